@@ -1,0 +1,217 @@
+"""Benchmark of the FlashAttention hot path on one MI355X.
+
+Workload (the headline): B=4, S=4096, H=32, D=128,
+bf16, causal, dropout 0; q, k, v, dO ~ N(0, 1) from torch.Generator('cpu')
+seed 42.  One step = forward + backward through the C ABI (fa_fwd, fa_bwd)
+with inputs resident in HBM.  Algorithmic FLOPs: F_fwd = 4*B*H*S*S*D/2,
+F_fwd+bwd = 3.5 * F_fwd.
+
+Prints ONE JSON line: value = fwd+bwd TFLOP/s; forward-only TFLOP/s, % of the
+dense bf16 MFMA peak, per-kernel times (HIP events on the launch stream), the
+roofline of the dominant kernel and the CPU baseline (the reference's PyTorch
+math path restated in oracle/, fp32 on this host, on a bounded sample of the
+same workload) ride along.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "flash-attn-v100_amd"))
+sys.path.insert(0, REPO)
+
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (AMD published)
+PEAK_HBM_GBS = 8000.0
+METRIC = "attention TFLOP/s fwd & fwd+bwd, bf16 S=4096 D=128 causal; % of MFMA peak"
+B, S, H, D = 4, 4096, 32, 128
+CAUSAL = True
+
+
+def f_fwd(b=B, h=H, s=S, d=D, causal=CAUSAL):
+    return 4.0 * b * h * s * s * d * (0.5 if causal else 1.0)
+
+
+def gpu_bench(steps: int, warmup: int):
+    import ctypes
+
+    import torch
+
+    from flash_attention_v100 import _lib
+
+    lib = _lib.load()
+    g = torch.Generator("cpu").manual_seed(42)
+    q, k, v, do = (torch.randn(B, S, H, D, generator=g, dtype=torch.float32).to(torch.bfloat16).cuda()
+                   for _ in range(4))
+    scale = D ** -0.5
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, S, device="cuda", dtype=torch.float32)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    fa = _lib.fwd_args(q, k, v, o, lse, None, CAUSAL, scale, 0.0, 0, 0)
+    ba = _lib.bwd_args(q, k, v, o, do, lse, dq, dk, dv, CAUSAL, scale, 0.0, 0, 0)
+    ws_bytes = lib.fa_bwd_workspace_size(ctypes.byref(ba))
+    ws = torch.empty(ws_bytes, device="cuda", dtype=torch.uint8)
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    wsp = ctypes.c_void_p(ws.data_ptr())
+
+    def fwd():
+        st = lib.fa_fwd(ctypes.byref(fa), sp)
+        if st:
+            raise RuntimeError(_lib.strerror(st))
+
+    def bwd_stage(s):
+        st = lib.fa_bwd_stage(ctypes.byref(ba), wsp, ws_bytes, s, sp)
+        if st:
+            raise RuntimeError(_lib.strerror(st))
+
+    def step():
+        fwd()
+        bwd_stage(-1)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # ---- timed region: exactly `steps` fwd+bwd steps ----
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t_step = (time.perf_counter() - t0) / steps
+
+    # ---- per-kernel averages with HIP events on the launch stream ----
+    def timed(fn, n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / n  # ms
+
+    n = max(steps, 10)
+    fwd_ms = timed(fwd, n)
+    delta_ms = timed(lambda: bwd_stage(0), n)
+    dkdv_ms = timed(lambda: bwd_stage(1), n)
+    dq_ms = timed(lambda: bwd_stage(2), n)
+    fwd_bwd_ms = timed(step, n)
+    ok = bool(torch.isfinite(o).all() and torch.isfinite(dq).all() and torch.isfinite(dk).all()
+              and torch.isfinite(dv).all())
+    return dict(t_step=t_step, fwd_ms=fwd_ms, delta_ms=delta_ms, dkdv_ms=dkdv_ms, dq_ms=dq_ms,
+                fwd_bwd_ms=fwd_bwd_ms, finite=ok, device=torch.cuda.get_device_name(0))
+
+
+def cpu_baseline(target_s: float = 12.0):
+    """The reference's math path (oracle.attention, fp32, autograd backward) on
+    this host's cores, on B=1 and as many heads of the workload as fit about
+    ``target_s`` seconds; reported with the same algorithmic FLOP count."""
+    import torch
+
+    from oracle import attention as oa
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator("cpu").manual_seed(42)
+
+    def run(h):
+        q, k, v, do = (torch.randn(1, S, h, D, generator=g, dtype=torch.float32) for _ in range(4))
+        t0 = time.perf_counter()
+        oa.attention_autograd(q, k, v, do, CAUSAL, D ** -0.5, dtype=torch.float32)
+        return time.perf_counter() - t0
+
+    run(1)  # warm-up
+    t1 = run(1)
+    h = int(max(1, min(H, target_s / max(t1, 1e-3))))
+    times = [run(h) for _ in range(2)]
+    t = min(times)
+    flop = 3.5 * f_fwd(b=1, h=h)
+    return {"value": round(flop / t / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"fwd+bwd of B=1, H={h} of the workload (S=4096, D=128, causal) in fp32 via "
+                      f"oracle.attention_autograd; best of 2 runs, {t:.2f} s each",
+            "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count()}
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the reference's multi-GPU helpers are out of scope)", file=sys.stderr)
+        sys.exit(2)
+
+    r = gpu_bench(a.steps, a.warmup)
+    F = f_fwd()
+    Ftot = 3.5 * F
+    value = Ftot / r["t_step"] / 1e12
+    fwd_tflops = F / (r["fwd_ms"] * 1e-3) / 1e12
+    kernels = {"fwd_kernel": r["fwd_ms"], "delta_kernel": r["delta_ms"], "dkdv_kernel": r["dkdv_ms"],
+               "dq_kernel": r["dq_ms"]}
+    # algorithmic FLOPs per launch: fwd = QK^T + PV; dkdv = 4 of the 5 backward GEMMs
+    # (QK^T recompute, dO V^T, P^T dO, dS^T Q); dq = dS K (its S/dP recompute is extra work)
+    algo = {"fwd_kernel": F, "dkdv_kernel": 2.0 * F, "dq_kernel": 0.5 * F}
+    dom = max(kernels, key=kernels.get)
+    if dom in algo:
+        ach = algo[dom] / (kernels[dom] * 1e-3) / 1e12
+        roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None}
+    else:
+        nbytes = 2 * B * S * H * D * 2 + 4 * B * H * S
+        ach = nbytes / (kernels[dom] * 1e-3) / 1e9
+        roof = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None}
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(r["t_step"] * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "C3: B=4 S=4096 H=32 D=128 bf16 causal, fwd+bwd (BASELINE configs[2])",
+                   "batch": B, "seq_len": S, "heads": H, "head_dim": D, "causal": CAUSAL,
+                   "parallelism": "single-gpu"},
+        "fwd_bwd_tflops": round(value, 2),
+        "fwd_bwd_pct_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "fwd_tflops": round(fwd_tflops, 2),
+        "fwd_pct_peak": round(100 * fwd_tflops / PEAK_BF16_TFLOPS, 2),
+        "kernel_ms": {kk: round(vv, 4) for kk, vv in kernels.items()},
+        "fwd_bwd_event_ms": round(r["fwd_bwd_ms"], 4),
+        "outputs_finite": r["finite"],
+        "device": r["device"],
+        "roofline": roof,
+    }
+    if not a.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,235 @@
+// Host side of the C ABI declared in include/fa_abi.h: argument validation
+// (pure host code, no HIP call before it passes) and dispatch to the dtype
+// launchers.  Stateless and re-entrant; launches on the caller's stream and
+// never synchronises.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "fa_abi.h"
+#include "fa_params.hpp"
+
+namespace {
+
+int elem_size(int32_t dtype) { return dtype == FA_DTYPE_F32 ? 4 : 2; }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// d stride 1; b, s, h strides non-negative multiples of 16 bytes
+int32_t check_strides(const int64_t st[4], int es) {
+    if (st[3] != 1) return FA_ERR_STRIDE;
+    for (int i = 0; i < 3; ++i)
+        if (st[i] < 0 || (st[i] * es) % 16 != 0) return FA_ERR_STRIDE;
+    return FA_OK;
+}
+
+int32_t check_common(int32_t B, int32_t Sq, int32_t Sk, int32_t H, int32_t Hkv, int32_t D, int32_t dtype,
+                     float scale, float dropout_p) {
+    if (B < 0 || Sq < 0 || Sk < 0 || H < 0 || Hkv < 0) return FA_ERR_SHAPE;
+    if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F32) return FA_ERR_DTYPE;
+    if (D != 32 && D != 64 && D != 128) return FA_ERR_HEAD_DIM;
+    if (H == 0 || Hkv == 0 || H % Hkv != 0) return FA_ERR_HEADS;
+    if (!std::isfinite(scale) || !(scale > 0.f)) return FA_ERR_SCALE;
+    if (!std::isfinite(dropout_p) || dropout_p < 0.f || dropout_p >= 1.f) return FA_ERR_DROPOUT;
+    // grid sizes: (ceil(S / 32) tiles) x heads x batch must fit a 32-bit grid
+    const int64_t tiles = ((int64_t)(Sq > Sk ? Sq : Sk) + 31) / 32;
+    if (tiles * (int64_t)H * (int64_t)B > 0x7fffffffLL) return FA_ERR_TOO_LARGE;
+    return FA_OK;
+}
+
+void split(const int64_t st[4], int64_t& sb, int64_t& ss, int64_t& sh) {
+    sb = st[0];
+    ss = st[1];
+    sh = st[2];
+}
+
+int32_t status_of(hipError_t e) { return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH; }
+
+}  // namespace
+
+extern "C" {
+
+int32_t fa_abi_version(void) { return FA_ABI_VERSION; }
+
+const char* fa_strerror(int32_t code) {
+    switch (code) {
+        case FA_OK: return "success";
+        case FA_ERR_NULL_ARG: return "a required pointer is NULL";
+        case FA_ERR_SHAPE: return "a size is negative or inconsistent";
+        case FA_ERR_HEAD_DIM: return "head_dim must be 32, 64 or 128";
+        case FA_ERR_DTYPE: return "dtype must be FA_DTYPE_F16, FA_DTYPE_BF16 or FA_DTYPE_F32";
+        case FA_ERR_STRIDE: return "the d stride must be 1 and the b/s/h strides multiples of 16 bytes";
+        case FA_ERR_HEADS: return "num_heads must be a positive multiple of num_heads_kv";
+        case FA_ERR_DROPOUT: return "dropout_p must be in [0, 1)";
+        case FA_ERR_WORKSPACE: return "workspace is NULL or smaller than fa_bwd_workspace_size";
+        case FA_ERR_ALIGN: return "tensor base pointers must be 16-byte aligned";
+        case FA_ERR_SCALE: return "scale must be finite and > 0";
+        case FA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
+        case FA_ERR_TOO_LARGE: return "problem too large for the kernel grid";
+        default: return "unknown status code";
+    }
+}
+
+int32_t fa_fwd_check(const fa_fwd_args* a) {
+    if (!a) return FA_ERR_NULL_ARG;
+    int32_t st = check_common(a->batch, a->seqlen_q, a->seqlen_k, a->num_heads, a->num_heads_kv, a->head_dim,
+                              a->dtype, a->scale, a->dropout_p);
+    if (st) return st;
+    const int64_t nq = (int64_t)a->batch * a->num_heads * a->seqlen_q;
+    if (nq == 0) return FA_OK;
+    if (!a->q || !a->o || !a->lse) return FA_ERR_NULL_ARG;
+    if (a->seqlen_k > 0 && (!a->k || !a->v)) return FA_ERR_NULL_ARG;
+    const int es = elem_size(a->dtype);
+    if ((st = check_strides(a->q_stride, es)) || (st = check_strides(a->k_stride, es)) ||
+        (st = check_strides(a->v_stride, es)) || (st = check_strides(a->o_stride, es)))
+        return st;
+    if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o)) return FA_ERR_ALIGN;
+    if (((uintptr_t)a->lse & 3u) || ((uintptr_t)a->max_vals & 3u)) return FA_ERR_ALIGN;
+    return FA_OK;
+}
+
+int32_t fa_fwd(const fa_fwd_args* a, void* stream) {
+    int32_t st = fa_fwd_check(a);
+    if (st) return st;
+    if ((int64_t)a->batch * a->num_heads * a->seqlen_q == 0) return FA_OK;
+    fa::FwdParams p{};
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.o = a->o;
+    p.lse = a->lse;
+    p.mx = a->max_vals;
+    split(a->q_stride, p.q_sb, p.q_ss, p.q_sh);
+    split(a->k_stride, p.k_sb, p.k_ss, p.k_sh);
+    split(a->v_stride, p.v_sb, p.v_ss, p.v_sh);
+    split(a->o_stride, p.o_sb, p.o_ss, p.o_sh);
+    p.B = a->batch;
+    p.Sq = a->seqlen_q;
+    p.Sk = a->seqlen_k;
+    p.H = a->num_heads;
+    p.Hkv = a->num_heads_kv;
+    p.group = a->num_heads / a->num_heads_kv;
+    p.scale = a->scale;
+    p.scale_log2 = a->scale * 1.4426950408889634f;
+    p.dropout_p = a->dropout_p;
+    p.rp = 1.f / (1.f - a->dropout_p);
+    p.seed = a->seed;
+    p.offset = a->offset;
+    const bool causal = a->causal != 0;
+    const bool dropout = a->dropout_p > 0.f;
+    hipStream_t s = (hipStream_t)stream;
+    switch (a->dtype) {
+        case FA_DTYPE_BF16: return status_of(fa::launch_fwd_bf16(p, a->head_dim, causal, dropout, s));
+        case FA_DTYPE_F16: return status_of(fa::launch_fwd_f16(p, a->head_dim, causal, dropout, s));
+        default: return status_of(fa::launch_fwd_f32(p, a->head_dim, causal, dropout, s));
+    }
+}
+
+size_t fa_bwd_workspace_size(const fa_bwd_args* a) {
+    if (!a) return 0;
+    if (check_common(a->batch, a->seqlen_q, a->seqlen_k, a->num_heads, a->num_heads_kv, a->head_dim, a->dtype,
+                     a->scale, a->dropout_p))
+        return 0;
+    const size_t n = (size_t)a->batch * (size_t)a->num_heads * (size_t)a->seqlen_q * sizeof(float);
+    return (n + 255) & ~(size_t)255;
+}
+
+int32_t fa_bwd_check(const fa_bwd_args* a, size_t ws_bytes) {
+    if (!a) return FA_ERR_NULL_ARG;
+    int32_t st = check_common(a->batch, a->seqlen_q, a->seqlen_k, a->num_heads, a->num_heads_kv, a->head_dim,
+                              a->dtype, a->scale, a->dropout_p);
+    if (st) return st;
+    const int64_t nq = (int64_t)a->batch * a->num_heads * a->seqlen_q;
+    const int64_t nk = (int64_t)a->batch * a->num_heads_kv * a->seqlen_k;
+    if (nq == 0 && nk == 0) return FA_OK;
+    if (nq > 0 && (!a->q || !a->o || !a->dout || !a->lse || !a->dq)) return FA_ERR_NULL_ARG;
+    if (nk > 0 && (!a->k || !a->v || !a->dk || !a->dv)) return FA_ERR_NULL_ARG;
+    const int es = elem_size(a->dtype);
+    const int64_t* strides[8] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride,
+                                 a->do_stride, a->dq_stride, a->dk_stride, a->dv_stride};
+    for (int i = 0; i < 8; ++i)
+        if ((st = check_strides(strides[i], es))) return st;
+    const void* ptrs[8] = {a->q, a->k, a->v, a->o, a->dout, a->dq, a->dk, a->dv};
+    for (int i = 0; i < 8; ++i)
+        if (!aligned16(ptrs[i])) return FA_ERR_ALIGN;
+    if ((uintptr_t)a->lse & 3u) return FA_ERR_ALIGN;
+    const size_t need = fa_bwd_workspace_size(a);
+    if (need > 0 && ws_bytes < need) return FA_ERR_WORKSPACE;
+    return FA_OK;
+}
+
+int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int32_t stage, void* stream) {
+    if (stage < -1 || stage > 2) return FA_ERR_SHAPE;
+    int32_t st = fa_bwd_check(a, ws_bytes);
+    if (st) return st;
+    const size_t need = fa_bwd_workspace_size(a);
+    if (need > 0 && (!workspace || !aligned16(workspace))) return FA_ERR_WORKSPACE;
+    if ((int64_t)a->batch * a->num_heads * a->seqlen_q == 0 &&
+        (int64_t)a->batch * a->num_heads_kv * a->seqlen_k == 0)
+        return FA_OK;
+    fa::BwdParams p{};
+    p.q = a->q;
+    p.k = a->k;
+    p.v = a->v;
+    p.o = a->o;
+    p.dout = a->dout;
+    p.lse = a->lse;
+    p.dq = a->dq;
+    p.dk = a->dk;
+    p.dv = a->dv;
+    p.delta = (float*)workspace;
+    split(a->q_stride, p.q_sb, p.q_ss, p.q_sh);
+    split(a->k_stride, p.k_sb, p.k_ss, p.k_sh);
+    split(a->v_stride, p.v_sb, p.v_ss, p.v_sh);
+    split(a->o_stride, p.o_sb, p.o_ss, p.o_sh);
+    split(a->do_stride, p.do_sb, p.do_ss, p.do_sh);
+    split(a->dq_stride, p.dq_sb, p.dq_ss, p.dq_sh);
+    split(a->dk_stride, p.dk_sb, p.dk_ss, p.dk_sh);
+    split(a->dv_stride, p.dv_sb, p.dv_ss, p.dv_sh);
+    p.B = a->batch;
+    p.Sq = a->seqlen_q;
+    p.Sk = a->seqlen_k;
+    p.H = a->num_heads;
+    p.Hkv = a->num_heads_kv;
+    p.group = a->num_heads / a->num_heads_kv;
+    p.scale = a->scale;
+    p.scale_log2 = a->scale * 1.4426950408889634f;
+    p.dropout_p = a->dropout_p;
+    p.rp = 1.f / (1.f - a->dropout_p);
+    p.seed = a->seed;
+    p.offset = a->offset;
+    const bool causal = a->causal != 0;
+    const bool dropout = a->dropout_p > 0.f;
+    hipStream_t s = (hipStream_t)stream;
+    switch (a->dtype) {
+        case FA_DTYPE_BF16: return status_of(fa::launch_bwd_bf16(p, a->head_dim, causal, dropout, stage, s));
+        case FA_DTYPE_F16: return status_of(fa::launch_bwd_f16(p, a->head_dim, causal, dropout, stage, s));
+        default: return status_of(fa::launch_bwd_f32(p, a->head_dim, causal, dropout, stage, s));
+    }
+}
+
+int32_t fa_bwd(const fa_bwd_args* a, void* workspace, size_t ws_bytes, void* stream) {
+    return fa_bwd_stage(a, workspace, ws_bytes, -1, stream);
+}
+
+int32_t fa_dropout_mask(uint64_t seed, uint64_t offset, int32_t B, int32_t H, int32_t Sq, int32_t Sk,
+                        float dropout_p, uint8_t* keep, void* stream) {
+    if (B < 0 || H < 0 || Sq < 0 || Sk < 0) return FA_ERR_SHAPE;
+    if (!std::isfinite(dropout_p) || dropout_p < 0.f || dropout_p >= 1.f) return FA_ERR_DROPOUT;
+    const int64_t n = (int64_t)B * H * Sq * Sk;
+    if (n == 0) return FA_OK;
+    if (!keep) return FA_ERR_NULL_ARG;
+    if ((n + 255) / 256 > 0x7fffffffLL) return FA_ERR_TOO_LARGE;
+    return status_of(fa::launch_dropout_mask(seed, offset, B, H, Sq, Sk, dropout_p, keep, (hipStream_t)stream));
+}
+
+int32_t fa_rand(uint64_t seed, const uint64_t* counters, int64_t n, float* u, void* stream) {
+    if (n < 0) return FA_ERR_SHAPE;
+    if (n == 0) return FA_OK;
+    if (!counters || !u) return FA_ERR_NULL_ARG;
+    if ((n + 255) / 256 > 0x7fffffffLL) return FA_ERR_TOO_LARGE;
+    return status_of(fa::launch_rand(seed, counters, n, u, (hipStream_t)stream));
+}
+
+}  // extern "C"

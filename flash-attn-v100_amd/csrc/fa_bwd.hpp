@@ -1,0 +1,520 @@
+// FlashAttention backward for gfx950 (reference: kernels/backward_kernel.py:17-205,
+// whose racy low-precision dQ read-modify-write and per-tile-pair delta are
+// replaced).  Three deterministic kernels, no atomics:
+//   1. delta_kernel: delta = rowsum(dO * O) in fp32, (B, H, Sq).
+//   2. dkdv_kernel: one workgroup per 128 keys of one (batch, KV head); wave w
+//      owns keys k0 + 32w .. +31 (lane l owns key k0 + 32w + l%32), K and V rows
+//      stay in registers; 32-query tiles of Q, dO, LSE, delta stream through
+//      double-buffered LDS.  Scores are computed as S = Q K^T so each lane holds
+//      queries {8(r/4) + 4(l/32) + r%4} of ITS key, which is exactly the MFMA
+//      B-operand layout needed for dV^T = dO^T P and dK^T = Q^T dS (the dO^T /
+//      Q^T operands come from row-major LDS through ds_read_b64_tr_b16).
+//      Query heads sharing a KV head are summed in-register.
+//   3. dq_kernel: one workgroup per 128 queries of one (batch, head), like the
+//      forward: S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T with Q, dO, LSE,
+//      delta held per lane; K/V tiles stream through double-buffered LDS.
+// All five products accumulate in fp32 and are rounded once to the input dtype.
+#pragma once
+
+#include "fa_common.hpp"
+#include "fa_params.hpp"
+
+namespace fa {
+
+// ---------------------------------------------------------------------------
+// delta = rowsum(dO * O)
+template <typename T, int D>
+__global__ __launch_bounds__(256) void delta_kernel(const BwdParams p) {
+    constexpr int EPC = 16 / sizeof(T);
+    constexpr int LPR = D / EPC;        // lanes per row
+    constexpr int RPB = 256 / LPR;      // rows per block
+    const int tid = threadIdx.x;
+    const int64_t row = (int64_t)blockIdx.x * RPB + tid / LPR;
+    const int part = tid % LPR;
+    const int64_t nrows = (int64_t)p.B * p.Sq * p.H;
+    float acc = 0.f;
+    int b = 0, i = 0, h = 0;
+    if (row < nrows) {
+        h = (int)(row % p.H);
+        const int64_t bi = row / p.H;
+        i = (int)(bi % p.Sq);
+        b = (int)(bi / p.Sq);
+        const T* orow = (const T*)p.o + b * p.o_sb + (int64_t)i * p.o_ss + h * p.o_sh + part * EPC;
+        const T* drow = (const T*)p.dout + b * p.do_sb + (int64_t)i * p.do_ss + h * p.do_sh + part * EPC;
+        const uint4 ov = *reinterpret_cast<const uint4*>(orow);
+        const uint4 dv = *reinterpret_cast<const uint4*>(drow);
+        if constexpr (Elem<T>::kF32) {
+            const f32x4 a = __builtin_bit_cast(f32x4, ov), c = __builtin_bit_cast(f32x4, dv);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc += a[e] * c[e];
+        } else {
+            const s16x8 a = __builtin_bit_cast(s16x8, ov), c = __builtin_bit_cast(s16x8, dv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc += Elem<T>::unpack1(a[e]) * Elem<T>::unpack1(c[e]);
+        }
+    }
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (row < nrows && part == 0) p.delta[((int64_t)b * p.H + h) * p.Sq + i] = acc;
+}
+
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+struct DkdvCfg {
+    static constexpr bool F32 = Elem<T>::kF32;
+    static constexpr int NW = 4;
+    static constexpr int NT = 64 * NW;
+    static constexpr int BK = 32 * NW;              // keys per workgroup
+    static constexpr int BQ = 32;                   // queries per tile
+    static constexpr int RW = D + (F32 ? 4 : 8);    // Q / dO row stride (elements)
+    static constexpr int QTILE = BQ * RW;
+    // per buffer: Q tile, dO tile, then lse2[BQ] and delta[BQ] as floats
+    static constexpr int BUF_BYTES = 2 * QTILE * (int)sizeof(T) + 2 * BQ * 4;
+    static constexpr int OW = D + (F32 ? 4 : 8);    // output staging stride
+    static constexpr int SMEM_BYTES_RAW = 2 * BUF_BYTES;
+    static constexpr int STAGE_BYTES = NW * 32 * OW * (int)sizeof(T);
+    static constexpr int SMEM_BYTES = SMEM_BYTES_RAW > STAGE_BYTES ? SMEM_BYTES_RAW : STAGE_BYTES;
+};
+
+template <typename T, int D, bool CAUSAL, bool DROPOUT>
+__global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const int n_ktiles) {
+    using C = DkdvCfg<T, D>;
+    constexpr int BQ = C::BQ, RW = C::RW;
+    __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6, l32 = lane & 31, hi = lane >> 5;
+    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int bhk = L / n_ktiles;
+    const int kt = L - bhk * n_ktiles;
+    const int hk = bhk % p.Hkv, b = bhk / p.Hkv;
+    const int k0 = kt * C::BK;
+    const int kw0 = k0 + 32 * w;
+    const int kj = kw0 + l32;  // this lane's key
+
+    // ---- K, V rows of this lane's key in registers (MFMA B operands) ----
+    constexpr int KR = C::F32 ? D / 8 : D / 16;
+    uint4 kreg[KR], vreg[KR];
+    {
+        const T* krow = (const T*)p.k + b * p.k_sb + (int64_t)kj * p.k_ss + hk * p.k_sh;
+        const T* vrow = (const T*)p.v + b * p.v_sb + (int64_t)kj * p.v_ss + hk * p.v_sh;
+#pragma unroll
+        for (int i = 0; i < KR; ++i) {
+            const int d0 = C::F32 ? hi * (D / 2) + 4 * i : 16 * i + 8 * hi;
+            const bool ok = kj < p.Sk;
+            kreg[i] = ok ? *reinterpret_cast<const uint4*>(krow + d0) : make_uint4(0u, 0u, 0u, 0u);
+            vreg[i] = ok ? *reinterpret_cast<const uint4*>(vrow + d0) : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+
+    f32x16 dk[D / 32], dv[D / 32];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) { dk[i] = f32x16{}; dv[i] = f32x16{}; }
+    const float c = p.scale_log2;
+
+    // query tiles: causal needs queries >= k0 only
+    const int qt_begin = CAUSAL ? (k0 / BQ) : 0;
+    const int qt_end = (p.Sq + BQ - 1) / BQ;
+    const int nq = qt_end > qt_begin ? qt_end - qt_begin : 0;
+    const int total = nq * p.group;  // (head in group) x (query tile)
+
+    TileStage<T, BQ, D, C::NT> qst, dost;
+    float lse_r = 0.f, del_r = 0.f;  // staged by threads tid < BQ
+    auto buf = [&](int s) -> char* { return smem + s * C::BUF_BYTES; };
+    auto issue = [&](int it) {
+        const int hh = hk * p.group + it / nq;
+        const int qb0 = (qt_begin + it % nq) * BQ;
+        const T* qb = (const T*)p.q + b * p.q_sb + (int64_t)qb0 * p.q_ss + hh * p.q_sh;
+        const T* db = (const T*)p.dout + b * p.do_sb + (int64_t)qb0 * p.do_ss + hh * p.do_sh;
+        qst.load(qb, p.q_ss, p.Sq - qb0, tid);
+        dost.load(db, p.do_ss, p.Sq - qb0, tid);
+        if (tid < BQ) {
+            const int q = qb0 + tid;
+            const int64_t si = ((int64_t)b * p.H + hh) * p.Sq + q;
+            lse_r = q < p.Sq ? p.lse[si] * kLog2e : INFINITY;  // tail queries: P = 0
+            del_r = q < p.Sq ? p.delta[si] : 0.f;
+        }
+    };
+    auto commit = [&](int s) {
+        char* bp = buf(s);
+        qst.template store<RW>((T*)bp, tid);
+        dost.template store<RW>((T*)bp + C::QTILE, tid);
+        float* f = (float*)(bp + 2 * C::QTILE * sizeof(T));
+        if (tid < BQ) { f[tid] = lse_r; f[BQ + tid] = del_r; }
+    };
+
+    if (total > 0) { issue(0); commit(0); }
+    for (int it = 0; it < total; ++it) {
+        if (it + 1 < total) issue(it + 1);
+        __syncthreads();
+        const char* bp = buf(it & 1);
+        const T* Qs = (const T*)bp;
+        const T* Ds = Qs + C::QTILE;
+        const float* lse2 = (const float*)(bp + 2 * C::QTILE * sizeof(T));
+        const float* dels = lse2 + BQ;
+        const int hh = hk * p.group + it / nq;
+        const int qb0 = (qt_begin + it % nq) * BQ;
+
+        const bool active = !CAUSAL || qb0 + BQ - 1 >= kw0;
+        if (active && kw0 < p.Sk) {
+            // ---- S = Q K^T and dP = dO V^T (C[q][key]) ----
+            f32x16 s = f32x16{}, dp = f32x16{};
+            const T* qrow = Qs + l32 * RW;
+            const T* drow = Ds + l32 * RW;
+            if constexpr (C::F32) {
+#pragma unroll
+                for (int i = 0; i < KR; ++i) {
+                    const f32x4 aq = *reinterpret_cast<const f32x4*>(qrow + hi * (D / 2) + 4 * i);
+                    const f32x4 ad = *reinterpret_cast<const f32x4*>(drow + hi * (D / 2) + 4 * i);
+                    const f32x4 bk = __builtin_bit_cast(f32x4, kreg[i]);
+                    const f32x4 bv = __builtin_bit_cast(f32x4, vreg[i]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        s = mfma_f32(aq[e], bk[e], s);
+                        dp = mfma_f32(ad[e], bv[e], dp);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < KR; ++kk) {
+                    const s16x8 aq = *reinterpret_cast<const s16x8*>(qrow + 16 * kk + 8 * hi);
+                    const s16x8 ad = *reinterpret_cast<const s16x8*>(drow + 16 * kk + 8 * hi);
+                    s = Elem<T>::mfma(aq, __builtin_bit_cast(s16x8, kreg[kk]), s);
+                    dp = Elem<T>::mfma(ad, __builtin_bit_cast(s16x8, vreg[kk]), dp);
+                }
+            }
+            // ---- P, dS ----
+            const bool need_mask = CAUSAL && qb0 < kw0 + 31;
+            uint64_t col_ctr = 0;
+            if (DROPOUT) col_ctr = p.offset + (uint64_t)(b * p.H + hh) * (uint64_t)p.Sq * (uint64_t)p.Sk + (uint64_t)kj;
+            float pd[16];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse2 + 8 * g + 4 * hi);
+                const f32x4 d4 = *reinterpret_cast<const f32x4*>(dels + 8 * g + 4 * hi);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * g + e;
+                    const int q = qb0 + 8 * g + 4 * hi + e;
+                    float pv = fast_exp2(__builtin_fmaf(s[r], c, -l4[e]));
+                    if (need_mask && q < kj) pv = 0.f;
+                    float dpv = dp[r];
+                    float pdv = pv;
+                    if (DROPOUT) {
+                        const float u = philox_uniform(p.seed, col_ctr + (uint64_t)q * (uint64_t)p.Sk);
+                        const float z = u > p.dropout_p ? p.rp : 0.f;
+                        dpv *= z;
+                        pdv *= z;
+                    }
+                    pd[r] = pdv;
+                    s[r] = pv * (dpv - d4[e]);  // dS (scale applied at the end)
+                }
+            }
+            // ---- dV^T += dO^T P,  dK^T += Q^T dS ----
+            if constexpr (C::F32) {
+#pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    const int qr = 8 * (t >> 2) + 4 * hi + (t & 3);
+#pragma unroll
+                    for (int i = 0; i < D / 32; ++i) {
+                        dv[i] = mfma_f32(Ds[qr * RW + 32 * i + l32], pd[t], dv[i]);
+                        dk[i] = mfma_f32(Qs[qr * RW + 32 * i + l32], s[t], dk[i]);
+                    }
+                }
+            } else {
+                const int trow = 4 * hi + ((lane & 15) >> 2);
+                const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+#pragma unroll
+                for (int ks = 0; ks < BQ / 16; ++ks) {
+                    float tp[8], ts[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) { tp[e] = pd[8 * ks + e]; ts[e] = s[8 * ks + e]; }
+                    const s16x8 bp8 = pack8<T>(tp);
+                    const s16x8 bs8 = pack8<T>(ts);
+#pragma unroll
+                    for (int i = 0; i < D / 32; ++i) {
+                        const int off = (16 * ks + trow) * RW + 32 * i + tcol;
+                        const s16x8 ad = cat4(lds_read_tr16(Ds + off), lds_read_tr16(Ds + off + 8 * RW));
+                        const s16x8 aq = cat4(lds_read_tr16(Qs + off), lds_read_tr16(Qs + off + 8 * RW));
+                        dv[i] = Elem<T>::mfma(ad, bp8, dv[i]);
+                        dk[i] = Elem<T>::mfma(aq, bs8, dk[i]);
+                    }
+                }
+            }
+        }
+        if (it + 1 < total) commit((it + 1) & 1);
+    }
+
+    // ---- epilogue: stage dK^T, dV^T through LDS as rows, coalesced stores ----
+    constexpr int OW = C::OW;
+    constexpr int EPC = 16 / sizeof(T);
+    constexpr int CPR = D / EPC;
+    T* Os = (T*)smem + w * 32 * OW;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        __syncthreads();
+        const f32x16* acc = pass == 0 ? dk : dv;
+        const float mul = pass == 0 ? p.scale : 1.f;
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = 32 * i + 8 * g + 4 * hi;
+                if constexpr (C::F32) {
+                    f32x4 v4;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v4[e] = acc[i][4 * g + e] * mul;
+                    *reinterpret_cast<f32x4*>(Os + l32 * OW + d) = v4;
+                } else {
+                    s16x4 v4;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v4[e] = Elem<T>::pack1(acc[i][4 * g + e] * mul);
+                    *reinterpret_cast<s16x4*>(Os + l32 * OW + d) = v4;
+                }
+            }
+        __syncthreads();
+        T* gbase = pass == 0 ? (T*)p.dk + b * p.dk_sb + hk * p.dk_sh : (T*)p.dv + b * p.dv_sb + hk * p.dv_sh;
+        const int64_t gss = pass == 0 ? p.dk_ss : p.dv_ss;
+#pragma unroll
+        for (int i = 0; i < 32 * CPR / 64; ++i) {
+            const int cidx = lane + 64 * i;
+            const int row = cidx / CPR, col = cidx % CPR;
+            const int key = kw0 + row;
+            if (key < p.Sk)
+                *reinterpret_cast<uint4*>(gbase + (int64_t)key * gss + col * EPC) =
+                    *reinterpret_cast<const uint4*>(Os + row * OW + col * EPC);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+struct DqCfg {
+    static constexpr bool F32 = Elem<T>::kF32;
+    static constexpr int NW = 4;
+    static constexpr int NT = 64 * NW;
+    static constexpr int BM = 32 * NW;            // queries per workgroup
+    static constexpr int BN = 32;                 // keys per tile
+    static constexpr int KW = D + (F32 ? 4 : 8);  // K / V row stride (elements)
+    static constexpr int KTILE = BN * KW;
+    static constexpr int OW = D + (F32 ? 4 : 8);
+    static constexpr int SMEM_ELEMS_RAW = 4 * KTILE;  // K, V double buffered
+    static constexpr int STAGE_ELEMS = NW * 32 * OW;
+    static constexpr int SMEM_ELEMS = SMEM_ELEMS_RAW > STAGE_ELEMS ? SMEM_ELEMS_RAW : STAGE_ELEMS;
+    // fp32 at D=128 needs more than 256 registers per lane (Q, dO and dQ^T in fp32)
+    static constexpr int MIN_BLOCKS = (F32 && D == 128) ? 1 : 2;
+};
+
+template <typename T, int D, bool CAUSAL, bool DROPOUT>
+__global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(const BwdParams p, const int n_qtiles) {
+    using C = DqCfg<T, D>;
+    constexpr int BN = C::BN, KW = C::KW;
+    __shared__ __attribute__((aligned(16))) T smem[C::SMEM_ELEMS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6, l32 = lane & 31, hi = lane >> 5;
+    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = L / n_qtiles;
+    const int qt = n_qtiles - 1 - (L - bh * n_qtiles);
+    const int h = bh % p.H, b = bh / p.H;
+    const int hk = h / p.group;
+    const int q0 = qt * C::BM;
+    const int qw0 = q0 + 32 * w;
+    const int qi = qw0 + l32;
+
+    constexpr int QR = C::F32 ? D / 8 : D / 16;
+    uint4 qreg[QR], doreg[QR];
+    {
+        const T* qrow = (const T*)p.q + b * p.q_sb + (int64_t)qi * p.q_ss + h * p.q_sh;
+        const T* drow = (const T*)p.dout + b * p.do_sb + (int64_t)qi * p.do_ss + h * p.do_sh;
+#pragma unroll
+        for (int i = 0; i < QR; ++i) {
+            const int d0 = C::F32 ? hi * (D / 2) + 4 * i : 16 * i + 8 * hi;
+            const bool ok = qi < p.Sq;
+            qreg[i] = ok ? *reinterpret_cast<const uint4*>(qrow + d0) : make_uint4(0u, 0u, 0u, 0u);
+            doreg[i] = ok ? *reinterpret_cast<const uint4*>(drow + d0) : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    const int64_t si = ((int64_t)b * p.H + h) * p.Sq + qi;
+    const float lse2 = qi < p.Sq ? p.lse[si] * kLog2e : INFINITY;
+    const float del = qi < p.Sq ? p.delta[si] : 0.f;
+    const float c = p.scale_log2;
+    uint64_t row_ctr = 0;
+    if (DROPOUT) row_ctr = p.offset + ((uint64_t)(b * p.H + h) * (uint64_t)p.Sq + (uint64_t)qi) * (uint64_t)p.Sk;
+
+    f32x16 dq[D / 32];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) dq[i] = f32x16{};
+
+    int kv_end = p.Sk;
+    if (CAUSAL) kv_end = min(kv_end, min(q0 + C::BM, p.Sq));
+    const int n_tiles = (kv_end + BN - 1) / BN;
+
+    const T* kbase = (const T*)p.k + b * p.k_sb + hk * p.k_sh;
+    const T* vbase = (const T*)p.v + b * p.v_sb + hk * p.v_sh;
+    TileStage<T, BN, D, C::NT> kst, vst;
+    T* Ks0 = smem;
+    T* Vs0 = smem + 2 * C::KTILE;
+    if (n_tiles > 0) {
+        kst.load(kbase, p.k_ss, p.Sk, tid);
+        vst.load(vbase, p.v_ss, p.Sk, tid);
+        kst.template store<KW>(Ks0, tid);
+        vst.template store<KW>(Vs0, tid);
+    }
+    for (int j = 0; j < n_tiles; ++j) {
+        const int k0 = j * BN;
+        if (j + 1 < n_tiles) {
+            kst.load(kbase + (int64_t)(k0 + BN) * p.k_ss, p.k_ss, p.Sk - (k0 + BN), tid);
+            vst.load(vbase + (int64_t)(k0 + BN) * p.v_ss, p.v_ss, p.Sk - (k0 + BN), tid);
+        }
+        __syncthreads();
+        const T* Ks = Ks0 + (j & 1) * C::KTILE;
+        const T* Vs = Vs0 + (j & 1) * C::KTILE;
+        const bool active = !CAUSAL || k0 <= qw0 + 31;
+        if (active) {
+            f32x16 s = f32x16{}, dp = f32x16{};
+            const T* krow = Ks + l32 * KW;
+            const T* vrow = Vs + l32 * KW;
+            if constexpr (C::F32) {
+#pragma unroll
+                for (int i = 0; i < QR; ++i) {
+                    const f32x4 ak = *reinterpret_cast<const f32x4*>(krow + hi * (D / 2) + 4 * i);
+                    const f32x4 av = *reinterpret_cast<const f32x4*>(vrow + hi * (D / 2) + 4 * i);
+                    const f32x4 bq = __builtin_bit_cast(f32x4, qreg[i]);
+                    const f32x4 bd = __builtin_bit_cast(f32x4, doreg[i]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        s = mfma_f32(ak[e], bq[e], s);
+                        dp = mfma_f32(av[e], bd[e], dp);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < QR; ++kk) {
+                    const s16x8 ak = *reinterpret_cast<const s16x8*>(krow + 16 * kk + 8 * hi);
+                    const s16x8 av = *reinterpret_cast<const s16x8*>(vrow + 16 * kk + 8 * hi);
+                    s = Elem<T>::mfma(ak, __builtin_bit_cast(s16x8, qreg[kk]), s);
+                    dp = Elem<T>::mfma(av, __builtin_bit_cast(s16x8, doreg[kk]), dp);
+                }
+            }
+            const bool need_mask = (k0 + BN > p.Sk) || (CAUSAL && k0 + BN - 1 > qw0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + 8 * (r >> 2) + 4 * hi + (r & 3);
+                float pv = fast_exp2(__builtin_fmaf(s[r], c, -lse2));
+                if (need_mask && (key >= p.Sk || (CAUSAL && key > qi))) pv = 0.f;
+                float dpv = dp[r];
+                if (DROPOUT) {
+                    const float u = philox_uniform(p.seed, row_ctr + (uint64_t)key);
+                    dpv *= u > p.dropout_p ? p.rp : 0.f;
+                }
+                s[r] = pv * (dpv - del);  // dS
+            }
+            if constexpr (C::F32) {
+#pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    const T* kr = Ks + (8 * (t >> 2) + 4 * hi + (t & 3)) * KW + l32;
+#pragma unroll
+                    for (int i = 0; i < D / 32; ++i) dq[i] = mfma_f32(kr[32 * i], s[t], dq[i]);
+                }
+            } else {
+                const int trow = 4 * hi + ((lane & 15) >> 2);
+                const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+#pragma unroll
+                for (int ks = 0; ks < BN / 16; ++ks) {
+                    float ts[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ts[e] = s[8 * ks + e];
+                    const s16x8 bs8 = pack8<T>(ts);
+#pragma unroll
+                    for (int i = 0; i < D / 32; ++i) {
+                        const T* src = Ks + (16 * ks + trow) * KW + 32 * i + tcol;
+                        const s16x8 a = cat4(lds_read_tr16(src), lds_read_tr16(src + 8 * KW));
+                        dq[i] = Elem<T>::mfma(a, bs8, dq[i]);
+                    }
+                }
+            }
+        }
+        if (j + 1 < n_tiles) {
+            kst.template store<KW>(Ks0 + ((j + 1) & 1) * C::KTILE, tid);
+            vst.template store<KW>(Vs0 + ((j + 1) & 1) * C::KTILE, tid);
+        }
+    }
+
+    __syncthreads();
+    constexpr int OW = C::OW;
+    T* Os = smem + w * 32 * OW;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = 32 * i + 8 * g + 4 * hi;
+            if constexpr (C::F32) {
+                f32x4 v4;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v4[e] = dq[i][4 * g + e] * p.scale;
+                *reinterpret_cast<f32x4*>(Os + l32 * OW + d) = v4;
+            } else {
+                s16x4 v4;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v4[e] = Elem<T>::pack1(dq[i][4 * g + e] * p.scale);
+                *reinterpret_cast<s16x4*>(Os + l32 * OW + d) = v4;
+            }
+        }
+    __syncthreads();
+    constexpr int EPC = 16 / sizeof(T);
+    constexpr int CPR = D / EPC;
+    T* gbase = (T*)p.dq + b * p.dq_sb + h * p.dq_sh;
+#pragma unroll
+    for (int i = 0; i < 32 * CPR / 64; ++i) {
+        const int cidx = lane + 64 * i;
+        const int row = cidx / CPR, col = cidx % CPR;
+        const int q = qw0 + row;
+        if (q < p.Sq)
+            *reinterpret_cast<uint4*>(gbase + (int64_t)q * p.dq_ss + col * EPC) =
+                *reinterpret_cast<const uint4*>(Os + row * OW + col * EPC);
+    }
+}
+
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool CAUSAL, bool DROPOUT>
+hipError_t launch_bwd_t(const BwdParams& p, int stage, hipStream_t s) {
+    if (stage < 0 || stage == 0) {
+        constexpr int EPC = 16 / sizeof(T);
+        constexpr int RPB = 256 / (D / EPC);
+        const int64_t nrows = (int64_t)p.B * p.Sq * p.H;
+        const int64_t nb = (nrows + RPB - 1) / RPB;
+        if (nb > 0) hipLaunchKernelGGL((delta_kernel<T, D>), dim3((unsigned)nb), dim3(256), 0, s, p);
+    }
+    if (stage < 0 || stage == 1) {
+        using C = DkdvCfg<T, D>;
+        const int nk = (p.Sk + C::BK - 1) / C::BK;
+        const int64_t nb = (int64_t)nk * p.Hkv * p.B;
+        if (nb > 0) hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, DROPOUT>), dim3((unsigned)nb), dim3(C::NT), 0, s, p, nk);
+    }
+    if (stage < 0 || stage == 2) {
+        using C = DqCfg<T, D>;
+        const int nq = (p.Sq + C::BM - 1) / C::BM;
+        const int64_t nb = (int64_t)nq * p.H * p.B;
+        if (nb > 0) hipLaunchKernelGGL((dq_kernel<T, D, CAUSAL, DROPOUT>), dim3((unsigned)nb), dim3(C::NT), 0, s, p, nq);
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_bwd_dispatch(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s) {
+#define FA_BWD_CASE(DD)                                                                  \
+    if (D == DD) {                                                                       \
+        if (causal) return dropout ? launch_bwd_t<T, DD, true, true>(p, stage, s)               \
+                                   : launch_bwd_t<T, DD, true, false>(p, stage, s);             \
+        return dropout ? launch_bwd_t<T, DD, false, true>(p, stage, s)                          \
+                       : launch_bwd_t<T, DD, false, false>(p, stage, s);                        \
+    }
+    FA_BWD_CASE(32)
+    FA_BWD_CASE(64)
+    FA_BWD_CASE(128)
+#undef FA_BWD_CASE
+    return hipErrorInvalidValue;
+}
+
+}  // namespace fa

@@ -1,0 +1,169 @@
+// Device-side building blocks shared by the gfx950 attention kernels.
+//
+// Wave64 MFMA operand layouts used throughout (checked on gfx950):
+//   v_mfma_f32_32x32x16_{bf16,f16}: lane l holds A[l%32][8*(l/32) + e] and
+//     B[8*(l/32) + e][l%32] for e = 0..7; accumulator r (0..15) of lane l is
+//     C[8*(r/4) + 4*(l/32) + r%4][l%32].
+//   v_mfma_f32_32x32x2_f32: lane l holds A[l%32][l/32], B[l/32][l%32]; same C.
+//   ds_read_b64_tr_b16: inside each 16-lane group, output lane i element e is
+//     element i%4 of the 8 bytes addressed by lane 4*e + i/4 of the group.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---------------------------------------------------------------------------
+// element traits
+template <typename T> struct Elem;
+template <> struct Elem<bf16> {
+    static constexpr bool kF32 = false;
+    using Vec8 = bf16x8;
+    __device__ static inline f32x16 mfma(const s16x8& a, const s16x8& b, const f32x16& c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    }
+    __device__ static inline short pack1(float x) { return __builtin_bit_cast(short, (bf16)x); }
+    __device__ static inline float unpack1(short x) { return (float)__builtin_bit_cast(bf16, x); }
+};
+template <> struct Elem<f16> {
+    static constexpr bool kF32 = false;
+    using Vec8 = f16x8;
+    __device__ static inline f32x16 mfma(const s16x8& a, const s16x8& b, const f32x16& c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+    __device__ static inline short pack1(float x) { return __builtin_bit_cast(short, (f16)x); }
+    __device__ static inline float unpack1(short x) { return (float)__builtin_bit_cast(f16, x); }
+};
+template <> struct Elem<float> {
+    static constexpr bool kF32 = true;
+};
+
+__device__ inline f32x16 mfma_f32(float a, float b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// 8 x 16-bit elements <-> 8 floats
+template <typename T>
+__device__ inline s16x8 pack8(const float* x) {
+    s16x8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = Elem<T>::pack1(x[e]);
+    return r;
+}
+
+// value held by lane l^32 (VALU permlane; both halves exchange)
+__device__ inline float swap_halves(float x) {
+    auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x),
+                                               false, false);
+    // lanes < 32 receive the upper half's value in the second slot, lanes >= 32
+    // receive the lower half's value in the first slot
+    return (threadIdx.x & 32) ? __builtin_bit_cast(float, p[0]) : __builtin_bit_cast(float, p[1]);
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------------------
+// LDS access
+typedef __attribute__((address_space(3))) void lds_void;
+
+// p must point into __shared__ memory (8-byte aligned); the cast is an
+// address-space cast, not an integer reinterpretation.
+__device__ inline s16x4 lds_read_tr16(const void* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+}
+
+__device__ inline s16x8 cat4(const s16x4& a, const s16x4& b) {
+    s16x8 r;
+    r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
+    r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// Philox4x32-10 (Salmon et al., SC'11) with Triton's tl.rand conventions:
+// key = (lo32 seed, hi32 seed), counter = (lo32 c, hi32 c, 0, 0); word 0 is
+// bit-cast to int32, folded x < 0 ? -x - 1 : x, and scaled by 4.6566127342e-10.
+__device__ inline uint32_t philox_word0(uint64_t seed, uint64_t ctr) {
+    uint32_t c0 = (uint32_t)ctr, c1 = (uint32_t)(ctr >> 32), c2 = 0u, c3 = 0u;
+    uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        const uint32_t hb = __umulhi(0xCD9E8D57u, c2), lb = 0xCD9E8D57u * c2;
+        const uint32_t ha = __umulhi(0xD2511F53u, c0), la = 0xD2511F53u * c0;
+        c0 = hb ^ c1 ^ k0;
+        c2 = ha ^ c3 ^ k1;
+        c1 = lb;
+        c3 = la;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    return c0;
+}
+
+__device__ inline float philox_uniform(uint64_t seed, uint64_t ctr) {
+    int32_t x = (int32_t)philox_word0(seed, ctr);
+    x = x < 0 ? -x - 1 : x;
+    return __fmul_rn((float)x, 4.6566127342e-10f);
+}
+
+// ---------------------------------------------------------------------------
+// Workgroup-id remap so that consecutive logical tiles land on one XCD.
+// Hardware dispatches workgroup L to XCD L % 8; logical id = (L % 8) * per + L / 8
+// keeps each XCD on a contiguous run of logical tiles (shared K/V stay in one L2).
+__device__ inline int xcd_remap(int L, int N) {
+    const int per = N >> 3;
+    const int full = per << 3;
+    if (L >= full) return L;
+    return (L & 7) * per + (L >> 3);
+}
+
+// ---------------------------------------------------------------------------
+// Global -> register -> LDS staging of a [ROWS][D] tile of T with 16-byte
+// chunks; rows >= nvalid are zero-filled.  LDS row stride LDSW elements.
+template <typename T, int ROWS, int D, int NT>
+struct TileStage {
+    static constexpr int EPC = 16 / sizeof(T);  // elements per 16-byte chunk
+    static constexpr int CPR = D / EPC;         // chunks per row
+    static constexpr int TOTAL = ROWS * CPR;
+    static constexpr int PER = (TOTAL + NT - 1) / NT;
+    uint4 r[PER];
+
+    __device__ inline void load(const T* __restrict__ base, int64_t row_stride, int nvalid, int tid) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int c = tid + i * NT;
+            const int row = c / CPR, col = c % CPR;
+            uint4 v = make_uint4(0u, 0u, 0u, 0u);
+            if ((TOTAL % NT == 0 || c < TOTAL) && row < nvalid)
+                v = *reinterpret_cast<const uint4*>(base + (int64_t)row * row_stride + col * EPC);
+            r[i] = v;
+        }
+    }
+    template <int LDSW>
+    __device__ inline void store(T* lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int c = tid + i * NT;
+            const int row = c / CPR, col = c % CPR;
+            if (TOTAL % NT == 0 || c < TOTAL)
+                *reinterpret_cast<uint4*>(lds + row * LDSW + col * EPC) = r[i];
+        }
+    }
+};
+
+}  // namespace fa

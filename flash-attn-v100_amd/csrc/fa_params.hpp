@@ -1,0 +1,68 @@
+// Kernel parameter blocks and launcher declarations shared by the host shim
+// (fa_abi.cpp) and the per-dtype kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+// Strides are in elements; the d stride is 1 (checked by the host shim).
+struct FwdParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;
+    float* mx;  // optional row max of the scaled scores
+    int64_t q_sb, q_ss, q_sh;
+    int64_t k_sb, k_ss, k_sh;
+    int64_t v_sb, v_ss, v_sh;
+    int64_t o_sb, o_ss, o_sh;
+    int B, Sq, Sk, H, Hkv, group;
+    int n_qtiles;
+    float scale;       // softmax scale
+    float scale_log2;  // scale * log2(e)
+    float dropout_p;
+    float rp;          // 1 / (1 - dropout_p)
+    uint64_t seed, offset;
+};
+
+struct BwdParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* o;
+    const void* dout;
+    const float* lse;
+    void* dq;
+    void* dk;
+    void* dv;
+    float* delta;  // workspace (B, H, Sq)
+    int64_t q_sb, q_ss, q_sh;
+    int64_t k_sb, k_ss, k_sh;
+    int64_t v_sb, v_ss, v_sh;
+    int64_t o_sb, o_ss, o_sh;
+    int64_t do_sb, do_ss, do_sh;
+    int64_t dq_sb, dq_ss, dq_sh;
+    int64_t dk_sb, dk_ss, dk_sh;
+    int64_t dv_sb, dv_ss, dv_sh;
+    int B, Sq, Sk, H, Hkv, group;
+    float scale, scale_log2, dropout_p, rp;
+    uint64_t seed, offset;
+};
+
+// dtype-specific launchers (fa_kernels_{bf16,f16,f32}.hip)
+hipError_t launch_fwd_bf16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
+hipError_t launch_fwd_f16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
+hipError_t launch_fwd_f32(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
+// stage: 0 = delta pre-pass, 1 = dK/dV, 2 = dQ, -1 = all three in order
+hipError_t launch_bwd_bf16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
+hipError_t launch_bwd_f16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
+hipError_t launch_bwd_f32(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
+// fa_misc.hip
+hipError_t launch_dropout_mask(uint64_t seed, uint64_t offset, int B, int H, int Sq, int Sk, float p,
+                               uint8_t* keep, hipStream_t s);
+hipError_t launch_rand(uint64_t seed, const uint64_t* ctr, int64_t n, float* u, hipStream_t s);
+
+}  // namespace fa

@@ -1,0 +1,226 @@
+"""ctypes binding of the gfx950 kernel library (``libfa_gfx950.so``).
+
+The library exports the C ABI of ``include/fa_abi.h``.  This module mirrors its
+argument structs, loads it (after torch, so that both share torch's HIP
+runtime: the library's ``libamdhip64.so.7`` dependency resolves to the copy
+torch already loaded) and turns status codes into exceptions.  All memory is
+allocated here with torch; the library itself never allocates.
+
+There is no fallback: if the library is missing or fails to load, every entry
+point raises :class:`FlashAttentionExtensionError`.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Tuple
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfa_gfx950.so")
+ABI_VERSION = 1
+HEAD_DIMS = (32, 64, 128)
+
+DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+_I64x4 = ctypes.c_int64 * 4
+
+
+class FlashAttentionExtensionError(ImportError):
+    """The HIP kernel library is missing or unusable (never silently bypassed)."""
+
+
+class FlashAttentionKernelError(RuntimeError):
+    """A C-ABI entry point returned a non-zero status."""
+
+    def __init__(self, fn: str, code: int, message: str):
+        super().__init__(f"{fn} failed with status {code}: {message}")
+        self.code = code
+
+
+class FwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("o", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p), ("max_vals", ctypes.c_void_p),
+        ("q_stride", _I64x4), ("k_stride", _I64x4), ("v_stride", _I64x4), ("o_stride", _I64x4),
+        ("batch", ctypes.c_int32), ("seqlen_q", ctypes.c_int32), ("seqlen_k", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32), ("num_heads_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("dtype", ctypes.c_int32), ("causal", ctypes.c_int32),
+        ("scale", ctypes.c_float), ("dropout_p", ctypes.c_float),
+        ("seed", ctypes.c_uint64), ("offset", ctypes.c_uint64),
+    ]
+
+
+class BwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("o", ctypes.c_void_p),
+        ("dout", ctypes.c_void_p), ("lse", ctypes.c_void_p),
+        ("dq", ctypes.c_void_p), ("dk", ctypes.c_void_p), ("dv", ctypes.c_void_p),
+        ("q_stride", _I64x4), ("k_stride", _I64x4), ("v_stride", _I64x4), ("o_stride", _I64x4),
+        ("do_stride", _I64x4), ("dq_stride", _I64x4), ("dk_stride", _I64x4), ("dv_stride", _I64x4),
+        ("batch", ctypes.c_int32), ("seqlen_q", ctypes.c_int32), ("seqlen_k", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32), ("num_heads_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("dtype", ctypes.c_int32), ("causal", ctypes.c_int32),
+        ("scale", ctypes.c_float), ("dropout_p", ctypes.c_float),
+        ("seed", ctypes.c_uint64), ("offset", ctypes.c_uint64),
+    ]
+
+
+EXPORTS = (
+    "fa_abi_version", "fa_strerror", "fa_fwd_check", "fa_fwd", "fa_bwd_workspace_size",
+    "fa_bwd_check", "fa_bwd", "fa_bwd_stage", "fa_dropout_mask", "fa_rand",
+)
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load (once) and type the library; raises FlashAttentionExtensionError."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FlashAttentionExtensionError(
+            f"gfx950 kernel library not found at {path}; build it with "
+            f"`python flash-attn-v100_amd/build.py`")
+    try:
+        lib = ctypes.CDLL(path)
+    except OSError as e:  # pragma: no cover - depends on the machine
+        raise FlashAttentionExtensionError(f"cannot load {path}: {e}") from e
+    P = ctypes.POINTER
+    lib.fa_abi_version.restype = ctypes.c_int32
+    lib.fa_abi_version.argtypes = []
+    lib.fa_strerror.restype = ctypes.c_char_p
+    lib.fa_strerror.argtypes = [ctypes.c_int32]
+    lib.fa_fwd_check.restype = ctypes.c_int32
+    lib.fa_fwd_check.argtypes = [P(FwdArgs)]
+    lib.fa_fwd.restype = ctypes.c_int32
+    lib.fa_fwd.argtypes = [P(FwdArgs), ctypes.c_void_p]
+    lib.fa_bwd_workspace_size.restype = ctypes.c_size_t
+    lib.fa_bwd_workspace_size.argtypes = [P(BwdArgs)]
+    lib.fa_bwd_check.restype = ctypes.c_int32
+    lib.fa_bwd_check.argtypes = [P(BwdArgs), ctypes.c_size_t]
+    lib.fa_bwd.restype = ctypes.c_int32
+    lib.fa_bwd.argtypes = [P(BwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.fa_bwd_stage.restype = ctypes.c_int32
+    lib.fa_bwd_stage.argtypes = [P(BwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_void_p]
+    lib.fa_dropout_mask.restype = ctypes.c_int32
+    lib.fa_dropout_mask.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int32, ctypes.c_int32,
+                                    ctypes.c_int32, ctypes.c_int32, ctypes.c_float, ctypes.c_void_p,
+                                    ctypes.c_void_p]
+    lib.fa_rand.restype = ctypes.c_int32
+    lib.fa_rand.argtypes = [ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+    v = lib.fa_abi_version()
+    if v != ABI_VERSION:
+        raise FlashAttentionExtensionError(f"{path} has ABI version {v}, expected {ABI_VERSION}")
+    _lib = lib
+    return lib
+
+
+def strerror(code: int) -> str:
+    return load().fa_strerror(code).decode()
+
+
+def _check(fn: str, code: int) -> None:
+    if code != 0:
+        raise FlashAttentionKernelError(fn, code, strerror(code))
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def prepare(t: torch.Tensor) -> torch.Tensor:
+    """Return ``t`` or a copy whose d stride is 1, whose other strides are
+    multiples of 16 bytes and whose base is 16-byte aligned (the kernels use
+    16-byte vector loads).  Counterpart of the reference's alignment clone
+    (kernels/forward_kernel.py:287-300), which re-aligned to 256 bytes."""
+    es = t.element_size()
+    ok = (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+          and all(s >= 0 and (s * es) % 16 == 0 for s in t.stride()[:-1]))
+    return t if ok else t.clone(memory_format=torch.contiguous_format)
+
+
+def _strides(t: torch.Tensor):
+    return _I64x4(*t.stride())
+
+
+def seed_offset(seed: Optional[int], offset: Optional[int]) -> Tuple[int, int]:
+    """Dropout Philox seed/offset; undrawn values come from torch's CPU
+    generator (no device synchronisation, reproducible under torch.manual_seed)."""
+    if seed is None:
+        seed = int(torch.randint(0, 2 ** 62, (1,), dtype=torch.int64).item())
+    if offset is None:
+        offset = 0
+    return int(seed) & 0xFFFFFFFFFFFFFFFF, int(offset) & 0xFFFFFFFFFFFFFFFF
+
+
+def fwd_args(q, k, v, o, lse, max_vals, causal, scale, dropout_p, seed, offset) -> FwdArgs:
+    B, Sq, H, D = q.shape
+    return FwdArgs(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+        max_vals.data_ptr() if max_vals is not None else None,
+        _strides(q), _strides(k), _strides(v), _strides(o),
+        B, Sq, k.shape[1], H, k.shape[2], D, DTYPE_CODES[q.dtype], int(bool(causal)),
+        float(scale), float(dropout_p), seed, offset)
+
+
+def fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: float,
+        dropout_p: float = 0.0, seed: int = 0, offset: int = 0, want_max: bool = False):
+    """Run ``fa_fwd``: returns (o, lse, max_vals or None).  Inputs (B, S, H, D)."""
+    lib = load()
+    q, k, v = prepare(q), prepare(k), prepare(v)
+    B, Sq, H, _ = q.shape
+    o = torch.empty_like(q, memory_format=torch.contiguous_format)
+    lse = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32)
+    mx = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32) if want_max else None
+    a = fwd_args(q, k, v, o, lse, mx, causal, scale, dropout_p, seed, offset)
+    _check("fa_fwd", lib.fa_fwd(ctypes.byref(a), _stream(q)))
+    return o, lse, mx
+
+
+def bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, offset) -> BwdArgs:
+    B, Sq, H, D = q.shape
+    return BwdArgs(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(),
+        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+        _strides(q), _strides(k), _strides(v), _strides(o), _strides(do),
+        _strides(dq), _strides(dk), _strides(dv),
+        B, Sq, k.shape[1], H, k.shape[2], D, DTYPE_CODES[q.dtype], int(bool(causal)),
+        float(scale), float(dropout_p), seed, offset)
+
+
+def bwd(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float = 0.0,
+        seed: int = 0, offset: int = 0):
+    """Run ``fa_bwd``: returns (dq, dk, dv) in the input dtype."""
+    lib = load()
+    q, k, v, o, do = (prepare(t) for t in (q, k, v, o, do))
+    lse = lse.contiguous()
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    a = bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, offset)
+    ws_bytes = lib.fa_bwd_workspace_size(ctypes.byref(a))
+    ws = torch.empty(max(int(ws_bytes), 256), device=q.device, dtype=torch.uint8)
+    _check("fa_bwd", lib.fa_bwd(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(q)))
+    return dq, dk, dv
+
+
+def dropout_mask(seed: int, offset: int, B: int, H: int, Sq: int, Sk: int, p: float,
+                 device="cuda") -> torch.Tensor:
+    """uint8 keep mask (B, H, Sq, Sk) from the kernels' device RNG."""
+    lib = load()
+    keep = torch.empty((B, H, Sq, Sk), device=device, dtype=torch.uint8)
+    _check("fa_dropout_mask", lib.fa_dropout_mask(seed, offset, B, H, Sq, Sk, float(p),
+                                                  ctypes.c_void_p(keep.data_ptr()), _stream(keep)))
+    return keep
+
+
+def rand(seed: int, counters: torch.Tensor) -> torch.Tensor:
+    """tl.rand(seed, counters) on the device; counters int64/uint64 device tensor."""
+    lib = load()
+    c = counters.contiguous()
+    u = torch.empty(c.shape, device=c.device, dtype=torch.float32)
+    _check("fa_rand", lib.fa_rand(seed, ctypes.c_void_p(c.data_ptr()), c.numel(),
+                                  ctypes.c_void_p(u.data_ptr()), _stream(c)))
+    return u

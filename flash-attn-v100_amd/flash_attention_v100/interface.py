@@ -1,0 +1,158 @@
+"""Public entry point with the reference's signature (``interface.py:199-349``).
+
+``flash_attention_v100(q, k, v, causal, scale, dropout_p, bias, block_size_m,
+block_size_n, enable_autotuning, return_softmax_lse, optimization_strategy,
+enable_multi_gpu, enable_profiling, fallback_on_error, validate_inputs)`` on
+(B, S, H, D) tensors returns O (B, Sq, H, D) in q's dtype, or ``(O, LSE)``.
+
+Single GPU only: the reference's Manager and its multi-GPU dispatch
+(``interface.py:25-196, 351-450``) are out of scope.  Validation checks
+metadata only (no full-tensor NaN scans, no host synchronisation; the
+reference's ``utils.py:227-254`` scans cost a sync each).
+
+Fallback (reference ``interface.py:331-348, 453-490``): with
+``fallback_on_error=True`` a request the gfx950 kernels do not implement
+(``NotImplementedError``: additive bias, an uncompiled head_dim) or reject as a
+tile hint (``ValueError`` from ``block_size_m/n``) is served by PyTorch math on
+the same GPU, with a warning.  Everything else raises: a missing kernel library
+(:class:`FlashAttentionExtensionError`), a kernel error, CPU tensors (there is
+no CPU path).
+"""
+from __future__ import annotations
+
+import math
+import warnings
+from typing import Optional, Tuple, Union
+
+import torch
+
+from . import _lib
+from .ops.attention import FlashAttentionV100Function, SUPPORTED_DTYPES, check_block_sizes
+
+_STRATEGIES = ("speed", "memory", "balanced", "adaptive")
+
+
+class _Stats:
+    """Counter of fallbacks taken (reference: Manager.error_recovery_count)."""
+    error_recovery_count = 0
+
+
+def validate_inputs_enhanced(q, k, v, scale=None, bias=None, dropout_p=0.0):
+    """Metadata checks with the reference's error types and messages
+    (``utils.py:31-160``); returns (q, k, v, scale) with the default
+    ``scale = head_dim ** -0.5`` (``utils.py:148-153``)."""
+    if not all(isinstance(t, torch.Tensor) for t in (q, k, v)):
+        raise TypeError("q, k, v must be torch.Tensor instances")
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("Input tensors must be 4-dimensional [batch, seq_len, num_heads, head_dim]")
+    B, Sq, Hq, Dq = q.shape
+    Bk, Sk, Hk, Dk = k.shape
+    Bv, Sv, Hv, Dv = v.shape
+    if not (B == Bk == Bv):
+        raise ValueError(f"Batch sizes must match across Q, K, V. Got Q: {B}, K: {Bk}, V: {Bv}")
+    if Sk != Sv:
+        raise ValueError(f"Sequence lengths of K and V must match. Got K: {Sk}, V: {Sv}")
+    if not (Dq == Dk == Dv):
+        raise ValueError(f"Head dimensions must match across Q, K, V. Got Q: {Dq}, K: {Dk}, V: {Dv}")
+    if Hk == 0 or Hv == 0 or Hq % Hk != 0 or Hq % Hv != 0:
+        raise ValueError(f"Number of query heads ({Hq}) must be divisible by number of key heads ({Hk}) "
+                         f"and value heads ({Hv})")
+    if Hk != Hv:
+        raise ValueError(f"Number of key heads ({Hk}) must equal number of value heads ({Hv})")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"All tensors must have the same dtype. Got Q: {q.dtype}, K: {k.dtype}, V: {v.dtype}")
+    if q.dtype not in SUPPORTED_DTYPES:
+        raise ValueError(f"Unsupported dtype {q.dtype}. Supported types: "
+                         + ", ".join(str(d) for d in SUPPORTED_DTYPES))
+    if not (q.device == k.device == v.device):
+        raise ValueError(f"All tensors must be on the same device. Got Q: {q.device}, K: {k.device}, V: {v.device}")
+    if q.device.type != "cuda":
+        raise ValueError("Flash Attention requires GPU tensors (there is no CPU path)")
+    if bias is not None:
+        if not isinstance(bias, torch.Tensor) or bias.dim() != 4:
+            raise ValueError("bias must be a 4-D tensor [batch|1, heads|1, seq_len_q, seq_len_k]")
+        if bias.shape[-2:] != (Sq, Sk) or bias.shape[0] not in (1, B) or bias.shape[1] not in (1, Hq):
+            raise ValueError(f"bias shape {tuple(bias.shape)} is not broadcastable to {(B, Hq, Sq, Sk)}")
+    if not (0.0 <= dropout_p < 1.0):
+        raise ValueError(f"dropout_p must be in [0.0, 1.0), got {dropout_p}")
+    if scale is None:
+        scale = Dq ** -0.5
+    if not (math.isfinite(scale) and scale > 0):
+        raise ValueError(f"scale must be finite and positive, got {scale}")
+    return q, k, v, scale
+
+
+def _fallback_to_pytorch(q, k, v, scale, causal, dropout_p, bias, return_softmax_lse):
+    """PyTorch math on the tensors' GPU, computed in float32 (reference
+    ``interface.py:453-490`` used SDPA).  Returns a real LSE, unlike the
+    reference's zeros.  Dropout here uses torch's RNG, not the kernels' Philox
+    stream."""
+    if q.device.type != "cuda":
+        raise ValueError("fallback requires GPU tensors")
+    H = q.shape[2]
+    rep = H // k.shape[2]
+    qf = q.float().transpose(1, 2)
+    kf = k.float().repeat_interleave(rep, dim=2).transpose(1, 2).contiguous()
+    vf = v.float().repeat_interleave(rep, dim=2).transpose(1, 2).contiguous()
+    s = torch.matmul(qf, kf.transpose(-2, -1).contiguous()) * scale
+    if bias is not None:
+        s = s + bias.float()
+    if causal:
+        mask = torch.triu(torch.ones(s.shape[-2], s.shape[-1], device=s.device, dtype=torch.bool), diagonal=1)
+        s = s.masked_fill(mask, float("-inf"))
+    lse = torch.logsumexp(s, dim=-1)
+    p = torch.softmax(s, dim=-1)
+    if dropout_p > 0:
+        p = torch.nn.functional.dropout(p, p=dropout_p, training=True)
+    o = torch.matmul(p, vf).transpose(1, 2).to(q.dtype)
+    return (o, lse) if return_softmax_lse else o
+
+
+def flash_attention_v100(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    causal: bool = False,
+    scale: Optional[float] = None,
+    dropout_p: float = 0.0,
+    bias: Optional[torch.Tensor] = None,
+    block_size_m: Optional[int] = None,
+    block_size_n: Optional[int] = None,
+    enable_autotuning: bool = True,
+    return_softmax_lse: bool = False,
+    optimization_strategy: str = "balanced",
+    enable_multi_gpu: Optional[bool] = None,
+    enable_profiling: bool = False,
+    fallback_on_error: bool = True,
+    validate_inputs: bool = True,
+    *,
+    dropout_seed: Optional[int] = None,
+    dropout_offset: Optional[int] = None,
+) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
+    """FlashAttention on (B, S, H, D) tensors; see the module docstring.
+
+    ``optimization_strategy`` (speed / memory / balanced / adaptive) selects
+    among numerically identical configurations and is validated only;
+    ``enable_multi_gpu`` and ``enable_profiling`` are accepted for signature
+    compatibility (single GPU; profile with rocprofv3).  ``dropout_seed`` /
+    ``dropout_offset`` pin the Philox stream of the dropout mask (drawn from
+    torch's CPU generator when omitted).
+    """
+    if optimization_strategy not in _STRATEGIES:
+        raise ValueError(f"optimization_strategy must be one of {_STRATEGIES}, got {optimization_strategy!r}")
+    if validate_inputs:
+        q, k, v, scale = validate_inputs_enhanced(q, k, v, scale, bias, dropout_p)
+    elif scale is None:
+        scale = q.shape[-1] ** -0.5
+    try:
+        check_block_sizes(block_size_m, block_size_n)
+        return FlashAttentionV100Function.apply(
+            q, k, v, scale, causal, dropout_p, bias, block_size_m, block_size_n,
+            enable_autotuning, return_softmax_lse, False, True, None, True,
+            optimization_strategy, False, 1, 0, dropout_seed, dropout_offset)
+    except (NotImplementedError, ValueError) as e:
+        if isinstance(e, _lib.FlashAttentionExtensionError) or not fallback_on_error:
+            raise
+        warnings.warn(f"Flash Attention failed ({e}), falling back to PyTorch implementation", UserWarning)
+        _Stats.error_recovery_count += 1
+        return _fallback_to_pytorch(q, k, v, scale, causal, dropout_p, bias, return_softmax_lse)

@@ -1,0 +1,175 @@
+/* C ABI of the MI355X (gfx950) FlashAttention library.
+ *
+ * Drop-in boundary for the hot path of mini-kio/flash-attn-v100: the Triton
+ * launchers that FlashAttentionV100Function calls.  Plain C types only; every
+ * buffer is device memory allocated by the caller (the library never
+ * allocates).  Work is enqueued on the caller's HIP stream; no call
+ * synchronises the host.
+ *
+ * Layout: q, o, dq, dout are (B, Sq, H, D); k, v, dk, dv are (B, Sk, Hkv, D);
+ * strides are in ELEMENTS in the order (b, s, h, d); the d stride must be 1,
+ * base pointers 16-byte aligned and the b/s/h strides multiples of 16 bytes.
+ * lse / max_vals are (B, H, Sq) float32, contiguous.
+ * Query head h reads KV head h / (H / Hkv).  Causal masks key j > query i
+ * (top-left aligned, also when Sq != Sk).
+ */
+#ifndef FA_ABI_H
+#define FA_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_ABI_VERSION 1
+
+/* element types */
+#define FA_DTYPE_F16 0
+#define FA_DTYPE_BF16 1
+#define FA_DTYPE_F32 2
+
+/* status codes (0 = success, negative = error; fa_strerror names them) */
+#define FA_OK 0
+#define FA_ERR_NULL_ARG -1    /* a required pointer is NULL */
+#define FA_ERR_SHAPE -2       /* a size is negative or inconsistent */
+#define FA_ERR_HEAD_DIM -3    /* head_dim not in {32, 64, 128} */
+#define FA_ERR_DTYPE -4       /* dtype code not FA_DTYPE_* */
+#define FA_ERR_STRIDE -5      /* d stride != 1, or b/s/h stride not a multiple of 16 bytes */
+#define FA_ERR_HEADS -6       /* num_heads not a positive multiple of num_heads_kv */
+#define FA_ERR_DROPOUT -7     /* dropout_p not in [0, 1) */
+#define FA_ERR_WORKSPACE -8   /* workspace NULL or smaller than fa_bwd_workspace_size */
+#define FA_ERR_ALIGN -9       /* a tensor base pointer is not 16-byte aligned */
+#define FA_ERR_SCALE -10      /* scale not finite and > 0 */
+#define FA_ERR_LAUNCH -11     /* the HIP runtime rejected a kernel launch */
+#define FA_ERR_TOO_LARGE -12  /* a grid dimension or index would overflow */
+
+/* Forward arguments.
+ * Replaces the launcher flash_attention_forward_triton_enhanced
+ * (kernels/forward_kernel.py:246-387) and its autotuned twin
+ * (kernels/forward_kernel.py:445-512), which FlashAttentionV100Function.forward
+ * calls at ops/attention.py:182-194.  Differences from the reference, all
+ * deliberate: lse is the true natural-log logsumexp of the scaled, masked
+ * scores (the reference stored the row sum there, forward_kernel.py:242);
+ * max_vals is the row max of the scaled scores, as there (:243); the dropout
+ * seed/offset are arguments instead of a device draw plus .item() host sync
+ * (:309-311). */
+typedef struct fa_fwd_args {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;      /* required */
+    float* max_vals; /* optional (NULL = not written) */
+    int64_t q_stride[4];
+    int64_t k_stride[4];
+    int64_t v_stride[4];
+    int64_t o_stride[4];
+    int32_t batch;
+    int32_t seqlen_q;
+    int32_t seqlen_k;
+    int32_t num_heads;
+    int32_t num_heads_kv;
+    int32_t head_dim;
+    int32_t dtype;
+    int32_t causal;
+    float scale;
+    float dropout_p;
+    uint64_t seed;
+    uint64_t offset;
+} fa_fwd_args;
+
+/* Backward arguments.
+ * Replaces flash_attention_backward_triton_enhanced
+ * (kernels/backward_kernel.py:208-318), called by
+ * FlashAttentionV100Function.backward at ops/attention.py:288-294.  It reads
+ * the saved (q, k, v, o, lse) plus the dropout seed/offset of the forward
+ * (the reference dropped them, ops/attention.py:209-227) and writes dq, dk,
+ * dv in the input dtype (fully overwritten, no zero-init needed). */
+typedef struct fa_bwd_args {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* o;
+    const void* dout;
+    const float* lse;
+    void* dq;
+    void* dk;
+    void* dv;
+    int64_t q_stride[4];
+    int64_t k_stride[4];
+    int64_t v_stride[4];
+    int64_t o_stride[4];
+    int64_t do_stride[4];
+    int64_t dq_stride[4];
+    int64_t dk_stride[4];
+    int64_t dv_stride[4];
+    int32_t batch;
+    int32_t seqlen_q;
+    int32_t seqlen_k;
+    int32_t num_heads;
+    int32_t num_heads_kv;
+    int32_t head_dim;
+    int32_t dtype;
+    int32_t causal;
+    float scale;
+    float dropout_p;
+    uint64_t seed;
+    uint64_t offset;
+} fa_bwd_args;
+
+/* Library ABI version (FA_ABI_VERSION).  No reference counterpart. */
+int32_t fa_abi_version(void);
+
+/* Static text for a status code.  No reference counterpart (the reference
+ * raised Python exceptions, utils.py:57-139). */
+const char* fa_strerror(int32_t code);
+
+/* Validate-only: returns the status fa_fwd would return for these arguments
+ * without launching anything (host-only; usable without a GPU). */
+int32_t fa_fwd_check(const fa_fwd_args* args);
+
+/* Forward: o, lse (and max_vals if non-NULL).  Replaces
+ * kernels/forward_kernel.py:246-387 (launch at :349-385). */
+int32_t fa_fwd(const fa_fwd_args* args, void* hip_stream);
+
+/* Bytes of device workspace fa_bwd needs (float32 delta = rowsum(dO * O),
+ * (B, H, Sq)); 0 on invalid arguments.  The reference had no workspace
+ * (it recomputed delta per tile pair, backward_kernel.py:119-121). */
+size_t fa_bwd_workspace_size(const fa_bwd_args* args);
+
+/* Validate-only counterpart of fa_bwd (host-only). */
+int32_t fa_bwd_check(const fa_bwd_args* args, size_t workspace_bytes);
+
+/* Backward: dq, dk, dv.  Replaces kernels/backward_kernel.py:208-318
+ * (launch at :279-316).  workspace: >= fa_bwd_workspace_size bytes,
+ * 256-byte aligned device memory. */
+int32_t fa_bwd(const fa_bwd_args* args, void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/* One stage of fa_bwd: 0 = delta pre-pass (writes the workspace), 1 = dK/dV,
+ * 2 = dQ; -1 = all three (same as fa_bwd).  Stages 1 and 2 only read the
+ * workspace and are independent of each other, so after stage 0 a caller may
+ * run them on two streams.  No reference counterpart (the reference had one
+ * fused Triton backward, kernels/backward_kernel.py:17-205). */
+int32_t fa_bwd_stage(const fa_bwd_args* args, void* workspace, size_t workspace_bytes, int32_t stage,
+                     void* hip_stream);
+
+/* Test hook: the dropout keep mask the kernels apply, keep[b][h][i][j] =
+ * U(seed, offset + ((b*H + h)*Sq + i)*Sk + j) > p, as uint8 (B, H, Sq, Sk),
+ * from the same device function the forward/backward use.  Counterpart of
+ * the tl.rand draw at kernels/forward_kernel.py:198-203 (with the row index
+ * i the reference omits restored). */
+int32_t fa_dropout_mask(uint64_t seed, uint64_t offset, int32_t batch, int32_t num_heads,
+                        int32_t seqlen_q, int32_t seqlen_k, float dropout_p,
+                        uint8_t* keep, void* hip_stream);
+
+/* Test hook: u[i] = tl.rand(seed, counters[i]) (Philox4x32-10 word 0 mapped
+ * to [0, 1) as Triton does), counters/u in device memory. */
+int32_t fa_rand(uint64_t seed, const uint64_t* counters, int64_t n, float* u, void* hip_stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_ABI_H */

@@ -1,0 +1,210 @@
+"""Restatement of the reference's attention math (TEST INFRASTRUCTURE ONLY).
+
+Device-agnostic torch code: run on the CPU it is the oracle; the GPU tests may
+also evaluate it in float64 on the device for shapes too large for the host.
+
+The reference computes attention in its test mock and its import fallback as
+plain PyTorch math on (B, S, H, D) tensors:
+
+* ``tests/test_attention.py:39-79``: transpose to (B, H, S, D), ``matmul(q, k^T)
+  * scale``, causal ``masked_fill(triu(ones, diagonal=1), -inf)``, ``softmax``,
+  optional dropout, ``matmul(p, v)``, transpose back.
+* ``__init__.py:34-55``: the same with ``q * scale`` folded before the matmul.
+* default ``scale = D ** -0.5`` (``utils.py:148-153``).
+
+The build fixes what the reference's Triton kernels get wrong
+(``kernels/forward_kernel.py:206-217`` normalisation, ``:242-243`` where ``L``
+holds the row sum, ``kernels/backward_kernel.py:176-194`` racy dQ): this oracle
+is the textbook math, with
+
+* LSE = natural-log logsumexp of the scaled, masked scores, shape (B, H, Sq);
+* dropout applied after the softmax normalisation, as ``Z / (1 - p)``, with
+  ``Z`` the keep mask of :func:`oracle.philox.dropout_keep_mask`
+  (reference: ``forward_kernel.py:198-203``, keep = ``u > p``);
+* causal masks key ``j > i`` (top-left aligned, ``forward_kernel.py:181``,
+  ``tests/test_attention.py:63``), also when Sq != Sk;
+* grouped KV heads: query head ``h`` reads KV head ``h // (H // Hkv)``
+  (``utils.py:88-97`` allows ``H % Hkv == 0``).
+
+Gradients follow ``kernels/backward_kernel.py:118-176`` with the row index of
+the dropout counter and the saved dropout mask restored:
+``delta_i = sum_d dO_id O_id``, ``dP = (dO V^T) * Z/(1-p)``,
+``dS = P * (dP - delta)``, ``dV = (P * Z/(1-p))^T dO``, ``dK = scale dS^T Q``,
+``dQ = scale dS K``.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+__all__ = [
+    "expand_kv",
+    "attention_forward",
+    "attention_backward",
+    "attention_autograd",
+    "brute_force_forward",
+    "flops",
+]
+
+
+def flops(B: int, H: int, Sq: int, Sk: int, D: int, causal: bool, bwd: bool = False) -> float:
+    """Algorithmic FLOPs: 4*B*H*Sq*Sk*D*(1/2 if causal); fwd+bwd = 3.5x that."""
+    f = 4.0 * B * H * Sq * Sk * D * (0.5 if causal else 1.0)
+    return f * 3.5 if bwd else f
+
+
+def expand_kv(x: torch.Tensor, num_heads: int) -> torch.Tensor:
+    """(B, S, Hkv, D) -> (B, S, H, D): query head h uses KV head h // (H // Hkv)."""
+    hkv = x.shape[2]
+    if hkv == num_heads:
+        return x
+    if num_heads % hkv != 0:
+        raise ValueError(f"num_heads {num_heads} not divisible by kv heads {hkv}")
+    return x.repeat_interleave(num_heads // hkv, dim=2)
+
+
+def _causal_mask(sq: int, sk: int, device=None) -> torch.Tensor:
+    # True where masked: key j > query i (triu(ones, diagonal=1)).
+    return torch.triu(torch.ones(sq, sk, dtype=torch.bool, device=device), diagonal=1)
+
+
+def _scores(q, k, causal, scale, dtype):
+    qh = q.to(dtype).transpose(1, 2)  # (B, H, Sq, D)
+    kh = k.to(dtype).transpose(1, 2)
+    s = torch.matmul(qh, kh.transpose(-2, -1)) * scale
+    if causal:
+        s = s.masked_fill(_causal_mask(s.shape[-2], s.shape[-1], s.device), float("-inf"))
+    return s
+
+
+def attention_forward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    causal: bool = False,
+    scale: Optional[float] = None,
+    dropout_mask: Optional[torch.Tensor] = None,
+    dropout_p: float = 0.0,
+    dtype: torch.dtype = torch.float64,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Forward O (B, Sq, H, D) in ``dtype`` and LSE (B, H, Sq) in ``dtype``.
+
+    ``dropout_mask`` is a bool keep-mask (B, H, Sq, Sk) or None.
+    Rows with no unmasked key (only possible when Sk == 0) give O = 0 and
+    LSE = -inf.
+    """
+    B, Sq, H, D = q.shape
+    if scale is None:
+        scale = D ** -0.5
+    k = expand_kv(k, H)
+    v = expand_kv(v, H)
+    Sk = k.shape[1]
+    if Sk == 0:
+        return (torch.zeros(B, Sq, H, D, dtype=dtype, device=q.device),
+                torch.full((B, H, Sq), float("-inf"), dtype=dtype, device=q.device))
+    s = _scores(q, k, causal, scale, dtype)
+    lse = torch.logsumexp(s, dim=-1)
+    p = torch.exp(s - lse.unsqueeze(-1))
+    if dropout_p > 0.0:
+        if dropout_mask is None:
+            raise ValueError("dropout_p > 0 needs an explicit keep mask")
+        p = p * dropout_mask.to(dtype) / (1.0 - dropout_p)
+    o = torch.matmul(p, v.to(dtype).transpose(1, 2))  # (B, H, Sq, D)
+    return o.transpose(1, 2).contiguous(), lse
+
+
+def attention_backward(
+    q, k, v, o, do, lse,
+    causal: bool = False,
+    scale: Optional[float] = None,
+    dropout_mask: Optional[torch.Tensor] = None,
+    dropout_p: float = 0.0,
+    dtype: torch.dtype = torch.float64,
+):
+    """Explicit-formula backward (dQ, dK, dV) in ``dtype``; dK/dV summed over
+    the query heads that share a KV head."""
+    B, Sq, H, D = q.shape
+    Hkv = k.shape[2]
+    if scale is None:
+        scale = D ** -0.5
+    ke = expand_kv(k, H)
+    ve = expand_kv(v, H)
+    s = _scores(q, ke, causal, scale, dtype)
+    p = torch.exp(s - lse.to(dtype).unsqueeze(-1))  # (B, H, Sq, Sk)
+    if causal:
+        p = p.masked_fill(_causal_mask(Sq, ke.shape[1], p.device), 0.0)
+    qh = q.to(dtype).transpose(1, 2)
+    kh = ke.to(dtype).transpose(1, 2)
+    vh = ve.to(dtype).transpose(1, 2)
+    doh = do.to(dtype).transpose(1, 2)
+    oh = o.to(dtype).transpose(1, 2)
+    delta = (doh * oh).sum(-1, keepdim=True)  # (B, H, Sq, 1)
+    dp = torch.matmul(doh, vh.transpose(-2, -1))
+    pz = p
+    if dropout_p > 0.0:
+        z = dropout_mask.to(dtype) / (1.0 - dropout_p)
+        dp = dp * z
+        pz = p * z
+    ds = p * (dp - delta)
+    dv = torch.matmul(pz.transpose(-2, -1), doh)
+    dk = torch.matmul(ds.transpose(-2, -1), qh) * scale
+    dq = torch.matmul(ds, kh) * scale
+    dq = dq.transpose(1, 2).contiguous()
+    dk = dk.transpose(1, 2)
+    dv = dv.transpose(1, 2)
+    if Hkv != H:
+        g = H // Hkv
+        dk = dk.reshape(B, dk.shape[1], Hkv, g, D).sum(3)
+        dv = dv.reshape(B, dv.shape[1], Hkv, g, D).sum(3)
+    return dq, dk.contiguous(), dv.contiguous()
+
+
+def attention_autograd(
+    q, k, v, do,
+    causal: bool = False,
+    scale: Optional[float] = None,
+    dropout_mask: Optional[torch.Tensor] = None,
+    dropout_p: float = 0.0,
+    dtype: torch.dtype = torch.float64,
+):
+    """(O, LSE, dQ, dK, dV) with the gradients taken by torch.autograd through
+    :func:`attention_forward` (a second, independent route to the backward)."""
+    qq = q.detach().to(dtype).requires_grad_(True)
+    kk = k.detach().to(dtype).requires_grad_(True)
+    vv = v.detach().to(dtype).requires_grad_(True)
+    o, lse = attention_forward(qq, kk, vv, causal, scale, dropout_mask, dropout_p, dtype)
+    o.backward(do.to(dtype))
+    return o.detach(), lse.detach(), qq.grad, kk.grad, vv.grad
+
+
+def brute_force_forward(q, k, v, causal=False, scale=None, keep=None, dropout_p=0.0):
+    """Scalar-loop forward in Python floats for tiny shapes: an implementation
+    that shares no code with :func:`attention_forward` (used to pin it)."""
+    B, Sq, H, D = q.shape
+    Hkv = k.shape[2]
+    Sk = k.shape[1]
+    if scale is None:
+        scale = D ** -0.5
+    qf, kf, vf = q.double().tolist(), k.double().tolist(), v.double().tolist()
+    o = [[[[0.0] * D for _ in range(H)] for _ in range(Sq)] for _ in range(B)]
+    lse = [[[float("-inf")] * Sq for _ in range(H)] for _ in range(B)]
+    for b in range(B):
+        for h in range(H):
+            hk = h // (H // Hkv)
+            for i in range(Sq):
+                js = [j for j in range(Sk) if not (causal and j > i)]
+                if not js:
+                    continue
+                sc = {j: scale * sum(qf[b][i][h][d] * kf[b][j][hk][d] for d in range(D)) for j in js}
+                m = max(sc.values())
+                tot = sum(math.exp(x - m) for x in sc.values())
+                lse[b][h][i] = m + math.log(tot)
+                for j in js:
+                    w = math.exp(sc[j] - m) / tot
+                    if dropout_p > 0.0:
+                        w = w * (1.0 / (1.0 - dropout_p) if keep[b][h][i][j] else 0.0)
+                    for d in range(D):
+                        o[b][i][h][d] += w * vf[b][j][hk][d]
+    return torch.tensor(o, dtype=torch.float64), torch.tensor(lse, dtype=torch.float64)

@@ -1,0 +1,178 @@
+"""The C-ABI library on a machine without a GPU: it loads, exports exactly the
+functions include/fa_abi.h declares, its structs match the header as compiled
+by gcc, and argument validation returns the documented status codes without
+any device call."""
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+import torch
+
+from flash_attention_v100 import _lib
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "fa_abi.h")
+
+CODES = {name: int(val) for name, val in re.findall(r"#define (FA_(?:OK|ERR_\w+))\s+(-?\d+)", open(HEADER).read())}
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(fa_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_loads_and_version():
+    lib = _lib.load()
+    assert lib.fa_abi_version() == _lib.ABI_VERSION == 1
+
+
+def test_exports_every_declared_function():
+    decl = declared_functions()
+    assert set(decl) == set(_lib.EXPORTS), decl
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (fa_\w+)$", out, flags=re.M))
+    assert set(decl) <= exported
+    lib = _lib.load()
+    for name in decl:
+        assert hasattr(lib, name)
+
+
+def _c_layout():
+    src = r"""
+#include <stdio.h>
+#include <stddef.h>
+#include "fa_abi.h"
+#define F(S, m) printf(#S " " #m " %zu\n", offsetof(S, m));
+int main(void) {
+  printf("fa_fwd_args sizeof %zu\n", sizeof(fa_fwd_args));
+  printf("fa_bwd_args sizeof %zu\n", sizeof(fa_bwd_args));
+  F(fa_fwd_args, q) F(fa_fwd_args, max_vals) F(fa_fwd_args, q_stride) F(fa_fwd_args, o_stride)
+  F(fa_fwd_args, batch) F(fa_fwd_args, causal) F(fa_fwd_args, scale) F(fa_fwd_args, dropout_p)
+  F(fa_fwd_args, seed) F(fa_fwd_args, offset)
+  F(fa_bwd_args, dout) F(fa_bwd_args, lse) F(fa_bwd_args, dv) F(fa_bwd_args, do_stride)
+  F(fa_bwd_args, dv_stride) F(fa_bwd_args, batch) F(fa_bwd_args, causal) F(fa_bwd_args, scale)
+  F(fa_bwd_args, seed) F(fa_bwd_args, offset)
+  return 0;
+}
+"""
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "layout.c")
+        exe = os.path.join(d, "layout")
+        open(c, "w").write(src)
+        subprocess.run(["gcc", "-std=c11", "-I", os.path.dirname(HEADER), c, "-o", exe], check=True)
+        out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout
+    return {tuple(ln.split()[:2]): int(ln.split()[2]) for ln in out.splitlines()}
+
+
+def test_ctypes_structs_match_header():
+    lay = _c_layout()
+    assert lay[("fa_fwd_args", "sizeof")] == ctypes.sizeof(_lib.FwdArgs)
+    assert lay[("fa_bwd_args", "sizeof")] == ctypes.sizeof(_lib.BwdArgs)
+    for (s, m), off in lay.items():
+        if m == "sizeof":
+            continue
+        cls = _lib.FwdArgs if s == "fa_fwd_args" else _lib.BwdArgs
+        assert getattr(cls, m).offset == off, (s, m)
+
+
+def test_strerror_names_every_code():
+    for name, code in CODES.items():
+        msg = _lib.strerror(code)
+        assert msg and msg != "unknown status code", name
+    assert _lib.strerror(12345) == "unknown status code"
+
+
+# ----------------------------------------------------------------------------- validation
+
+def _cpu_fwd(B=2, Sq=64, Sk=64, H=4, Hkv=4, D=64, dtype=torch.float16):
+    q = torch.zeros(B, Sq, H, D, dtype=dtype)
+    k = torch.zeros(B, Sk, Hkv, D, dtype=dtype)
+    v = torch.zeros(B, Sk, Hkv, D, dtype=dtype)
+    o = torch.zeros_like(q)
+    lse = torch.zeros(B, H, Sq, dtype=torch.float32)
+    keep = (q, k, v, o, lse)
+    a = _lib.fwd_args(q, k, v, o, lse, None, True, D ** -0.5, 0.0, 0, 0)
+    return a, keep
+
+
+def _status(a):
+    return _lib.load().fa_fwd_check(ctypes.byref(a))
+
+
+def test_fwd_check_accepts_valid():
+    for dt in (torch.float16, torch.bfloat16, torch.float32):
+        for D in (32, 64, 128):
+            a, _ = _cpu_fwd(D=D, dtype=dt)
+            assert _status(a) == CODES["FA_OK"]
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("head_dim", 96, "FA_ERR_HEAD_DIM"),
+    ("head_dim", 256, "FA_ERR_HEAD_DIM"),
+    ("dtype", 7, "FA_ERR_DTYPE"),
+    ("batch", -1, "FA_ERR_SHAPE"),
+    ("seqlen_k", -3, "FA_ERR_SHAPE"),
+    ("num_heads_kv", 3, "FA_ERR_HEADS"),
+    ("num_heads_kv", 0, "FA_ERR_HEADS"),
+    ("dropout_p", 1.0, "FA_ERR_DROPOUT"),
+    ("dropout_p", -0.1, "FA_ERR_DROPOUT"),
+    ("dropout_p", float("nan"), "FA_ERR_DROPOUT"),
+    ("scale", 0.0, "FA_ERR_SCALE"),
+    ("scale", -1.0, "FA_ERR_SCALE"),
+    ("scale", float("inf"), "FA_ERR_SCALE"),
+    ("q", None, "FA_ERR_NULL_ARG"),
+    ("lse", None, "FA_ERR_NULL_ARG"),
+])
+def test_fwd_check_rejects(field, value, code):
+    a, _keep = _cpu_fwd()
+    setattr(a, field, value)
+    assert _status(a) == CODES[code]
+    # the launching entry point returns the same code and touches no device
+    assert _lib.load().fa_fwd(ctypes.byref(a), None) == CODES[code]
+
+
+def test_fwd_check_strides_and_alignment():
+    a, _keep = _cpu_fwd()
+    a.q_stride[3] = 2
+    assert _status(a) == CODES["FA_ERR_STRIDE"]
+    a, _keep = _cpu_fwd()
+    a.k_stride[1] = a.k_stride[1] + 1  # not a multiple of 16 bytes
+    assert _status(a) == CODES["FA_ERR_STRIDE"]
+    a, _keep = _cpu_fwd()
+    a.v = a.v + 2
+    assert _status(a) == CODES["FA_ERR_ALIGN"]
+
+
+def test_fwd_check_empty_problem_is_ok():
+    a, _keep = _cpu_fwd(Sq=0)
+    a.q = None
+    assert _status(a) == CODES["FA_OK"]
+
+
+def test_bwd_workspace_and_checks():
+    lib = _lib.load()
+    B, S, H, D = 2, 100, 3, 64
+    q = torch.zeros(B, S, H, D, dtype=torch.bfloat16)
+    lse = torch.zeros(B, H, S)
+    a = _lib.bwd_args(q, q, q, q, q, lse, q, q, q, True, 0.125, 0.0, 0, 0)
+    ws = lib.fa_bwd_workspace_size(ctypes.byref(a))
+    assert ws == ((B * H * S * 4 + 255) // 256) * 256
+    assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_OK"]
+    assert lib.fa_bwd_check(ctypes.byref(a), ws - 4) == CODES["FA_ERR_WORKSPACE"]
+    assert lib.fa_bwd_stage(ctypes.byref(a), None, ws, 3, None) == CODES["FA_ERR_SHAPE"]
+    assert lib.fa_bwd(ctypes.byref(a), None, ws, None) == CODES["FA_ERR_WORKSPACE"]
+    a.dq = None
+    assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_ERR_NULL_ARG"]
+
+
+def test_rng_hooks_validation():
+    lib = _lib.load()
+    assert lib.fa_dropout_mask(1, 0, 1, 1, 4, 4, 1.5, None, None) == CODES["FA_ERR_DROPOUT"]
+    assert lib.fa_dropout_mask(1, 0, 1, 1, 4, 4, 0.5, None, None) == CODES["FA_ERR_NULL_ARG"]
+    assert lib.fa_dropout_mask(1, 0, 0, 1, 4, 4, 0.5, None, None) == CODES["FA_OK"]
+    assert lib.fa_rand(1, None, -1, None, None) == CODES["FA_ERR_SHAPE"]
+    assert lib.fa_rand(1, None, 0, None, None) == CODES["FA_OK"]
+    assert lib.fa_rand(1, None, 5, None, None) == CODES["FA_ERR_NULL_ARG"]

@@ -1,0 +1,159 @@
+"""The public API on the GPU: flash_attention_v100, FlashAttentionV100Function
+and the kernel-level launchers, including the reference's own property tests
+(tests/test_attention.py:229-311, 352-379, 449-486, 602-625, 797-823)
+retargeted at the gfx950 kernels instead of the reference's in-file mock."""
+import warnings
+
+import pytest
+import torch
+
+import flash_attention_v100 as fa
+from flash_attention_v100 import _lib
+from helpers import assert_parity, c_keep_mask, compare, make_inputs
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+REF_SHAPES = [(2, 512, 8, 64), (1, 1024, 12, 64), (2, 2048, 16, 64), (1, 4096, 8, 128)]
+REF_DTYPES = [torch.float16, torch.float32, torch.bfloat16]
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def _qkv(shape, dtype, seed=42):
+    # reference fixture: randn, q and k scaled by D**-0.5 * 0.5 (tests/test_attention.py:249-283)
+    torch.manual_seed(seed)
+    B, S, H, D = shape
+    s = D ** -0.5 * 0.5
+    q = (torch.randn(B, S, H, D, device=DEV) * s).to(dtype)
+    k = (torch.randn(B, S, H, D, device=DEV) * s).to(dtype)
+    v = torch.randn(B, S, H, D, device=DEV).to(dtype)
+    return q, k, v
+
+
+@pytest.mark.parametrize("shape", REF_SHAPES)
+@pytest.mark.parametrize("dtype", REF_DTYPES)
+def test_forward_basic(shape, dtype):
+    say(f"case: api forward basic {shape} {dtype}")
+    q, k, v = _qkv(shape, dtype)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")  # no fallback may be taken
+        out = fa.flash_attention_v100(q, k, v)
+    assert out.shape == q.shape and out.dtype == dtype
+    assert torch.isfinite(out).all()
+    assert 0.01 < out.float().std().item() < 10
+
+
+@pytest.mark.parametrize("dtype", REF_DTYPES)
+def test_backward_basic(dtype):
+    say(f"case: api backward basic {dtype}")
+    q, k, v = (t.requires_grad_(True) for t in _qkv((2, 512, 8, 64), dtype))
+    out = fa.flash_attention_v100(q, k, v, causal=True)
+    out.float().sum().backward()
+    for g in (q.grad, k.grad, v.grad):
+        assert g is not None and torch.isfinite(g).all()
+        assert 1e-8 < g.float().norm().item() < 1e4
+
+
+def test_causal_differs_from_full():
+    q, k, v = _qkv((2, 512, 8, 64), torch.float16)
+    a = fa.flash_attention_v100(q, k, v, causal=False)
+    b = fa.flash_attention_v100(q, k, v, causal=True)
+    assert (a.float() - b.float()).abs().max().item() > 1e-6
+
+
+def test_strategies_agree():
+    q, k, v = _qkv((1, 1024, 12, 64), torch.bfloat16)
+    outs = [fa.flash_attention_v100(q, k, v, optimization_strategy=s) for s in
+            ("speed", "memory", "balanced", "adaptive")]
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+
+
+def test_interface_equals_kernel_and_lse():
+    say("case: interface vs C ABI")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(2, 300, 4, 128, torch.bfloat16))
+    o, lse = fa.flash_attention_v100(q, k, v, causal=True, return_softmax_lse=True)
+    o2, lse2, _ = _lib.fwd(q, k, v, True, 128 ** -0.5)
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    assert lse.shape == (2, 4, 300) and lse.dtype == torch.float32
+
+
+def test_autograd_function_matches_abi_and_oracle():
+    say("case: FlashAttentionV100Function autograd")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(2, 333, 4, 64, torch.float16, Hkv=2))
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o = fa.FlashAttentionV100Function.apply(qq, kk, vv, 0.125, True)
+    o.backward(do)
+    o2, lse2, _ = _lib.fwd(q, k, v, True, 0.125)
+    dq, dk, dv = _lib.bwd(q, k, v, o2, do, lse2, True, 0.125)
+    assert torch.equal(o, o2)
+    assert torch.equal(qq.grad, dq) and torch.equal(kk.grad, dk) and torch.equal(vv.grad, dv)
+    res = compare(q, k, v, do, True, 0.125, (o2, lse2, dq, dk, dv), ref_device="cpu")
+    assert_parity(res, torch.float16, "autograd GQA")
+
+
+def test_dropout_through_interface_is_reproducible_and_exact():
+    say("case: dropout via interface")
+    B, S, H, D, p = 1, 200, 2, 64, 0.1
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, S, H, D, torch.float32, seed=9))
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o = fa.flash_attention_v100(qq, kk, vv, causal=True, dropout_p=p, dropout_seed=42, dropout_offset=0)
+    o.backward(do)
+    o_again = fa.flash_attention_v100(q, k, v, causal=True, dropout_p=p, dropout_seed=42, dropout_offset=0)
+    assert torch.equal(o.detach(), o_again)
+    keep = torch.from_numpy(c_keep_mask(42, 0, B, H, S, S, p)).bool().to(DEV)
+    lse = _lib.fwd(q, k, v, True, D ** -0.5, p, 42, 0)[1]
+    res = compare(q, k, v, do, True, D ** -0.5, (o.detach(), lse, qq.grad, kk.grad, vv.grad),
+                  keep=keep, p=p, ref_device="cpu")
+    assert_parity(res, torch.float32, "dropout interface")
+
+
+def test_kernel_level_launchers():
+    q, k, v, do = (t.to(DEV) for t in make_inputs(1, 256, 2, 64, torch.bfloat16))
+    o, lse, mx = fa.flash_attention_forward_triton_enhanced(q, k, v, 0.125, True)
+    s = torch.matmul(q.float().transpose(1, 2), k.float().transpose(1, 2).transpose(-2, -1).contiguous()) * 0.125
+    s = s.masked_fill(torch.triu(torch.ones(256, 256, dtype=torch.bool, device=DEV), 1), float("-inf"))
+    assert torch.allclose(mx, s.amax(-1), atol=1e-4)
+    dq, dk, dv = fa.flash_attention_backward_triton_enhanced(q, k, v, o, do, lse, mx, 0.125, True)
+    o2, lse2, mx2 = fa.flash_attention_forward_autotuned_enhanced(q, k, v, 0.125, True)
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
+
+
+def test_invalid_tiles_fall_back_finite():
+    # reference tests/test_attention.py:602-625: an unusable tile falls back and stays finite
+    q, k, v = _qkv((1, 256, 4, 64), torch.float16)
+    with pytest.warns(UserWarning, match="falling back"):
+        out = fa.flash_attention_v100(q, k, v, block_size_m=10000, block_size_n=10000)
+    assert torch.isfinite(out).all()
+    with pytest.raises(ValueError):
+        fa.flash_attention_v100(q, k, v, block_size_m=10000, fallback_on_error=False)
+
+
+def test_bias_falls_back_to_device_math():
+    q, k, v = _qkv((1, 128, 4, 64), torch.float16)
+    bias = torch.randn(1, 4, 128, 128, device=DEV, dtype=torch.float16)
+    with pytest.warns(UserWarning, match="falling back"):
+        out = fa.flash_attention_v100(q, k, v, causal=True, bias=bias)
+    assert out.device.type == "cuda" and torch.isfinite(out).all()
+    with pytest.raises(NotImplementedError):
+        fa.flash_attention_v100(q, k, v, bias=bias, fallback_on_error=False)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("p", [0.0, 0.1])
+def test_causal_dropout_combinations_finite(causal, p):
+    q, k, v = _qkv((2, 256, 4, 64), torch.float16)
+    out = fa.flash_attention_v100(q, k, v, causal=causal, dropout_p=p)
+    assert torch.isfinite(out).all()
+
+
+def test_kernel_errors_raise_not_fall_back():
+    q, k, v = _qkv((1, 64, 2, 96), torch.float16)  # head_dim 96 is not compiled
+    with pytest.warns(UserWarning, match="falling back"):
+        fa.flash_attention_v100(q, k, v)
+    with pytest.raises(NotImplementedError):
+        fa.flash_attention_v100(q, k, v, fallback_on_error=False)

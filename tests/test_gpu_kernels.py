@@ -1,0 +1,203 @@
+"""Parity of the gfx950 kernels, called through the C ABI, against the oracle.
+
+Tolerance: fp16/bf16 outputs within 2x the error of the
+reference's own math run in the same dtype on the GPU (both against the
+float64 oracle); fp32 within 1e-5 of max|oracle|; dropout masks bit-exact.
+Small shapes use the CPU oracle; the BASELINE-size configs evaluate the same
+oracle functions in float64 on the GPU, one head chunk at a time.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from flash_attention_v100 import _lib
+from helpers import assert_parity, c_keep_mask, compare, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+DEV = "cuda"
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def run(q, k, v, do, causal, scale, p=0.0, seed=0, offset=0, bwd=True):
+    o, lse, _ = _lib.fwd(q, k, v, causal, scale, p, seed, offset)
+    if not bwd:
+        torch.cuda.synchronize()
+        return o, lse
+    dq, dk, dv = _lib.bwd(q, k, v, o, do, lse, causal, scale, p, seed, offset)
+    torch.cuda.synchronize()
+    return o, lse, dq, dk, dv
+
+
+# ----------------------------------------------------------------------------- RNG
+
+def test_rand_matches_triton_vectors():
+    say("case: fa_rand vs triton_rand_vectors.json")
+    with open(os.path.join(GOLDEN, "triton_rand_vectors.json")) as f:
+        cases = json.load(f)["cases"]
+    for c in cases:
+        ctr = torch.tensor(np.array(c["counters"], dtype=np.uint64).view(np.int64), device=DEV)
+        u = _lib.rand(c["seed"], ctr).cpu().numpy().view(np.uint32)
+        assert np.array_equal(u, np.array(c["uniform_f32_bits"], dtype=np.uint32)), c["seed"]
+
+
+@pytest.mark.parametrize("shape,seed,offset", [
+    ((8, 16, 1000, 1000), 42, 0),          # C5 mask
+    ((2, 3, 77, 129), 42, 2**32 - 5),      # counter crosses the 32-bit boundary
+    ((1, 2, 33, 65), 2**63 + 5, 2**64 - 100),  # 64-bit wrap of the counter
+])
+def test_dropout_mask_bit_exact(shape, seed, offset):
+    say(f"case: fa_dropout_mask {shape} seed={seed} offset={offset}")
+    B, H, Sq, Sk = shape
+    got = _lib.dropout_mask(seed, offset, B, H, Sq, Sk, 0.1).cpu().numpy()
+    want = c_keep_mask(seed, offset, B, H, Sq, Sk, 0.1)
+    assert np.array_equal(got, want)
+
+
+# ----------------------------------------------------------------------------- small shapes, CPU oracle
+
+SMALL = []
+for dt in (torch.float16, torch.bfloat16, torch.float32):
+    for D in (32, 64, 128):
+        for causal in (False, True):
+            SMALL.append((dt, 2, 200, 200, 3, 3, D, causal))
+SMALL += [
+    (torch.bfloat16, 1, 130, 257, 2, 2, 64, True),    # Sq < Sk
+    (torch.bfloat16, 1, 300, 77, 2, 2, 64, True),     # Sq > Sk (top-left causal)
+    (torch.float16, 1, 300, 77, 2, 2, 128, False),
+    (torch.bfloat16, 2, 160, 160, 4, 2, 128, True),   # GQA 2:1
+    (torch.float16, 1, 96, 96, 8, 1, 64, False),      # MQA
+    (torch.float32, 1, 150, 150, 4, 2, 64, True),     # fp32 GQA
+    (torch.bfloat16, 1, 1, 1, 2, 2, 64, True),        # single query / key
+    (torch.float16, 3, 1, 50, 2, 2, 32, False),       # decode-like
+    (torch.bfloat16, 1, 64, 1, 2, 2, 128, False),     # single key
+]
+
+
+def _id(c):
+    dt, B, Sq, Sk, H, Hkv, D, causal = c
+    return f"{str(dt)[6:]}-B{B}-Sq{Sq}-Sk{Sk}-H{H}-Hkv{Hkv}-D{D}-{'causal' if causal else 'full'}"
+
+
+@pytest.mark.parametrize("case", SMALL, ids=[_id(c) for c in SMALL])
+def test_small_fwd_bwd(case):
+    dt, B, Sq, Sk, H, Hkv, D, causal = case
+    say(f"case: small {_id(case)}")
+    q, k, v, do = make_inputs(B, Sq, H, D, dt, Sk=Sk, Hkv=Hkv, seed=7)
+    scale = D ** -0.5
+    outs = run(*(t.to(DEV) for t in (q, k, v, do)), causal, scale)
+    res = compare(*(t.to(DEV) for t in (q, k, v, do)), causal, scale, outs, ref_device="cpu")
+    assert_parity(res, dt, _id(case))
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_small_dropout(D):
+    B, S, H, p = 2, 150, 3, 0.2
+    say(f"case: small dropout D={D}")
+    for dt in (torch.float16, torch.float32):
+        q, k, v, do = (t.to(DEV) for t in make_inputs(B, S, H, D, dt, seed=11))
+        outs = run(q, k, v, do, True, D ** -0.5, p, seed=123, offset=456)
+        keep = torch.from_numpy(c_keep_mask(123, 456, B, H, S, S, p)).bool().to(DEV)
+        res = compare(q, k, v, do, True, D ** -0.5, outs, keep=keep, p=p, ref_device="cpu")
+        assert_parity(res, dt, f"dropout D={D} {dt}")
+
+
+# ----------------------------------------------------------------------------- BASELINE configs
+
+def test_c1_forward():
+    say("case: C1 (2,1024,12,64) fp16 non-causal fwd")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(2, 1024, 12, 64, torch.float16))
+    outs = run(q, k, v, do, False, 0.125, bwd=False)
+    res = compare(q, k, v, do, False, 0.125, outs, ref_device="cpu", with_bwd=False)
+    assert_parity(res, torch.float16, "C1")
+
+
+def test_c2_fwd_bwd():
+    say("case: C2 (2,1024,12,64) fp16 causal fwd+bwd")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(2, 1024, 12, 64, torch.float16))
+    outs = run(q, k, v, do, True, 0.125)
+    res = compare(q, k, v, do, True, 0.125, outs, ref_device="cpu")
+    assert_parity(res, torch.float16, "C2")
+
+
+def test_c3_fwd_bwd():
+    say("case: C3 (4,4096,32,128) bf16 causal fwd+bwd")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(4, 4096, 32, 128, torch.bfloat16))
+    scale = 128 ** -0.5
+    outs = run(q, k, v, do, True, scale)
+    res = compare(q, k, v, do, True, scale, outs, hpc=8)
+    assert_parity(res, torch.bfloat16, "C3")
+
+
+def test_c3_size_independent_invariants():
+    # sum_j P_ij = 1 => sum_j dV_j = sum_i dO_i ; sum_j dS_ij = 0 => sum_j dK_j = 0
+    say("case: C3 invariants")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(4, 4096, 32, 128, torch.bfloat16))
+    o, lse, dq, dk, dv = run(q, k, v, do, True, 128 ** -0.5)
+    s_dv = dv.double().sum(1)
+    s_do = do.double().sum(1)
+    assert (s_dv - s_do).abs().max().item() <= 2e-2 * s_do.abs().max().item()
+    s_dk = dk.double().sum(1)
+    assert s_dk.abs().max().item() <= 2e-2 * dk.double().abs().sum(1).max().item()
+    assert torch.isfinite(o).all() and torch.isfinite(lse).all() and torch.isfinite(dq).all()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_c4_long_sequence(causal):
+    say(f"case: C4 (1,16384,16,128) bf16 causal={causal} q,k~N(0,4)")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(1, 16384, 16, 128, torch.bfloat16, qk_scale=2.0))
+    scale = 128 ** -0.5
+    outs = run(q, k, v, do, causal, scale)
+    res = compare(q, k, v, do, causal, scale, outs, hpc=1)
+    assert_parity(res, torch.bfloat16, f"C4 causal={causal}")
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_c5_edge_sweep(D, dt):
+    say(f"case: C5 (8,1000,16,{D}) {dt} causal dropout 0.1 seed 42 offset 0")
+    B, S, H, p = 8, 1000, 16, 0.1
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, S, H, D, dt))
+    scale = D ** -0.5
+    keep_dev = _lib.dropout_mask(42, 0, B, H, S, S, p).bool()
+    keep = torch.from_numpy(c_keep_mask(42, 0, B, H, S, S, p)).bool().to(DEV)
+    assert torch.equal(keep_dev, keep)
+    outs = run(q, k, v, do, True, scale, p, seed=42, offset=0)
+    res = compare(q, k, v, do, True, scale, outs, keep=keep, p=p, hpc=8)
+    assert_parity(res, dt, f"C5 D={D}")
+
+
+def test_deterministic():
+    say("case: determinism (2,1024,8,128) bf16 causal, two runs")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(2, 1024, 8, 128, torch.bfloat16, seed=3))
+    a = run(q, k, v, do, True, 128 ** -0.5)
+    b = run(q, k, v, do, True, 128 ** -0.5)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_strided_inputs_match_contiguous():
+    say("case: (B,H,S,D)-major storage viewed as (B,S,H,D)")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(2, 256, 4, 64, torch.bfloat16, seed=5))
+    qs, ks, vs, dos = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v, do))
+    assert qs.stride() != q.stride()
+    a = run(q, k, v, do, True, 0.125)
+    b = run(qs, ks, vs, dos, True, 0.125)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_empty_keys():
+    say("case: Sk = 0")
+    q = torch.randn(1, 5, 2, 64, device=DEV, dtype=torch.float16)
+    k = torch.empty(1, 0, 2, 64, device=DEV, dtype=torch.float16)
+    o, lse, _ = _lib.fwd(q, k, k, False, 0.125)
+    torch.cuda.synchronize()
+    assert torch.equal(o, torch.zeros_like(o)) and bool((lse == float("-inf")).all())
