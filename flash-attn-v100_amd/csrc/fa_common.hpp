@@ -66,14 +66,10 @@ __device__ inline s16x8 pack8(const float* x) {
     return r;
 }
 
-// value held by lane l^32 (VALU permlane; both halves exchange)
-__device__ inline float swap_halves(float x) {
-    auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x),
-                                               false, false);
-    // lanes < 32 receive the upper half's value in the second slot, lanes >= 32
-    // receive the lower half's value in the first slot
-    return (threadIdx.x & 32) ? __builtin_bit_cast(float, p[0]) : __builtin_bit_cast(float, p[1]);
-}
+// value held by lane l^32.  (v_permlane32_swap with both operands equal to x
+// would do this in one VALU op, but the compiler folds the per-half select of
+// its two results to the first one, so the LDS-crossbar shuffle is used.)
+__device__ inline float swap_halves(float x) { return __shfl_xor(x, 32, 64); }
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
