@@ -150,13 +150,33 @@ def _cpu_model():
     return None
 
 
+def copy_calibration(gib: float = 1.0, reps: int = 5):
+    """A plain device copy of known size, for scaling rocprofv3's FETCH_SIZE /
+    WRITE_SIZE counters (KiB per dispatch) to bytes."""
+    import torch
+
+    n = int(gib * (1 << 30)) // 2
+    src = torch.ones(n, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n * 2, "copy_calibration_bytes_written": n * 2,
+                      "reps": reps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
     a = ap.parse_args()
+    if a.copy_calibration:
+        copy_calibration()
+        return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(the reference's multi-GPU helpers are out of scope)", file=sys.stderr)

@@ -49,6 +49,9 @@ def common_flags():
         "-I", CSRC,
         # keep the compiler from emitting packed-fp32 VALU ops (v_pk_*_f32)
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # keep MFMA accumulators in VGPR form: without it the register allocator
+        # parks the dK/dV accumulators in AGPRs and copies them every iteration
+        "-mllvm", "-amdgpu-mfma-vgpr-form=true",
         "-Wall",
         "-Wno-unused-command-line-argument",
     ]

@@ -8,13 +8,18 @@
 //      double-buffered LDS.  Scores are computed as S = Q K^T so each lane holds
 //      queries {8(r/4) + 4(l/32) + r%4} of ITS key, which is exactly the MFMA
 //      B-operand layout needed for dV^T = dO^T P and dK^T = Q^T dS (the dO^T /
-//      Q^T operands come from row-major LDS through ds_read_b64_tr_b16).
+//      Q^T operands come from the row-major LDS tiles via ds_read_b64_tr_b16;
+//      a second, transposed copy of the tiles measured slower here).
 //      Query heads sharing a KV head are summed in-register.
 //   3. dq_kernel: one workgroup per 128 queries of one (batch, head), like the
 //      forward: S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T with Q, dO, LSE,
-//      delta held per lane; K/V tiles stream through double-buffered LDS.
+//      delta held per lane; K/V tiles stream through double-buffered LDS (K
+//      both row-major and transposed).
+// Diagonal (causal) tiles run a separate masking variant of each tile step.
 // All five products accumulate in fp32 and are rounded once to the input dtype.
 #pragma once
+
+#include <type_traits>
 
 #include "fa_common.hpp"
 #include "fa_params.hpp"
@@ -66,9 +71,12 @@ struct DkdvCfg {
     static constexpr int NT = 64 * NW;
     static constexpr int BK = 32 * NW;              // keys per workgroup
     static constexpr int BQ = 32;                   // queries per tile
-    static constexpr int RW = D + (F32 ? 4 : 8);    // Q / dO row stride (elements)
+    // Q / dO row stride: odd multiple of 16 bytes (conflict-free ds_read_b128
+    // row reads) whose 4 consecutive rows of a ds_read_b64_tr_b16 do not overlap
+    // in the 256-byte bank window
+    static constexpr int RW = D + (F32 ? 4 : (D == 64 ? 8 : 24));
     static constexpr int QTILE = BQ * RW;
-    // per buffer: Q tile, dO tile, then lse2[BQ] and delta[BQ] as floats
+    // per buffer: Q rows, dO rows, then lse2[BQ] and delta[BQ] as floats
     static constexpr int BUF_BYTES = 2 * QTILE * (int)sizeof(T) + 2 * BQ * 4;
     static constexpr int OW = D + (F32 ? 4 : 8);    // output staging stride
     static constexpr int SMEM_BYTES_RAW = 2 * BUF_BYTES;
@@ -106,13 +114,15 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
             vreg[i] = ok ? *reinterpret_cast<const uint4*>(vrow + d0) : make_uint4(0u, 0u, 0u, 0u);
         }
     }
+    wait_vmem();
 
     f32x16 dk[D / 32], dv[D / 32];
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) { dk[i] = f32x16{}; dv[i] = f32x16{}; }
     const float c = p.scale_log2;
 
-    // query tiles: causal needs queries >= k0 only
+    // query tiles: causal needs queries >= k0 only; the first NMASK of them
+    // (per head) cross the key block and run the masking variant
     const int qt_begin = CAUSAL ? (k0 / BQ) : 0;
     const int qt_end = (p.Sq + BQ - 1) / BQ;
     const int nq = qt_end > qt_begin ? qt_end - qt_begin : 0;
@@ -143,10 +153,10 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
         if (tid < BQ) { f[tid] = lse_r; f[BQ + tid] = del_r; }
     };
 
-    if (total > 0) { issue(0); commit(0); }
-    for (int it = 0; it < total; ++it) {
+    auto step = [&](int it, auto mask_tag) {
+        constexpr bool MASK = decltype(mask_tag)::value;
         if (it + 1 < total) issue(it + 1);
-        __syncthreads();
+        lds_barrier();
         const char* bp = buf(it & 1);
         const T* Qs = (const T*)bp;
         const T* Ds = Qs + C::QTILE;
@@ -155,8 +165,8 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
         const int hh = hk * p.group + it / nq;
         const int qb0 = (qt_begin + it % nq) * BQ;
 
-        const bool active = !CAUSAL || qb0 + BQ - 1 >= kw0;
-        if (active && kw0 < p.Sk) {
+        const bool active = (!MASK || !CAUSAL || qb0 + BQ - 1 >= kw0) && kw0 < p.Sk;
+        if (active) {
             // ---- S = Q K^T and dP = dO V^T (C[q][key]) ----
             f32x16 s = f32x16{}, dp = f32x16{};
             const T* qrow = Qs + l32 * RW;
@@ -184,7 +194,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
                 }
             }
             // ---- P, dS ----
-            const bool need_mask = CAUSAL && qb0 < kw0 + 31;
+            const bool need_mask = MASK && CAUSAL && qb0 < kw0 + 31;
             uint64_t col_ctr = 0;
             if (DROPOUT) col_ctr = p.offset + (uint64_t)(b * p.H + hh) * (uint64_t)p.Sq * (uint64_t)p.Sk + (uint64_t)kj;
             float pd[16];
@@ -222,6 +232,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
                     }
                 }
             } else {
+                // dO^T / Q^T operands straight from the row-major tiles
                 const int trow = 4 * hi + ((lane & 15) >> 2);
                 const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
@@ -243,7 +254,12 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
             }
         }
         if (it + 1 < total) commit((it + 1) & 1);
-    }
+    };
+
+    if (total > 0) { issue(0); commit(0); }
+    // one loop body: a second (unmasked) copy of this 256-register body makes the
+    // register allocator shuffle the dK/dV accumulators through AGPRs
+    for (int it = 0; it < total; ++it) step(it, std::integral_constant<bool, CAUSAL>{});
 
     // ---- epilogue: stage dK^T, dV^T through LDS as rows, coalesced stores ----
     constexpr int OW = C::OW;
@@ -252,7 +268,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
     T* Os = (T*)smem + w * 32 * OW;
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
-        __syncthreads();
+        lds_barrier();
         const f32x16* acc = pass == 0 ? dk : dv;
         const float mul = pass == 0 ? p.scale : 1.f;
 #pragma unroll
@@ -272,7 +288,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
                     *reinterpret_cast<s16x4*>(Os + l32 * OW + d) = v4;
                 }
             }
-        __syncthreads();
+        lds_barrier();
         T* gbase = pass == 0 ? (T*)p.dk + b * p.dk_sb + hk * p.dk_sh : (T*)p.dv + b * p.dv_sb + hk * p.dv_sh;
         const int64_t gss = pass == 0 ? p.dk_ss : p.dv_ss;
 #pragma unroll
@@ -296,9 +312,12 @@ struct DqCfg {
     static constexpr int BM = 32 * NW;            // queries per workgroup
     static constexpr int BN = 32;                 // keys per tile
     static constexpr int KW = D + (F32 ? 4 : 8);  // K / V row stride (elements)
+    static constexpr int TW = BN + 8;             // K^T row stride (16-bit types)
     static constexpr int KTILE = BN * KW;
+    static constexpr int KTTILE = F32 ? 0 : D * TW;
+    static constexpr int BUF = 2 * KTILE + KTTILE;  // K rows, V rows, K^T
     static constexpr int OW = D + (F32 ? 4 : 8);
-    static constexpr int SMEM_ELEMS_RAW = 4 * KTILE;  // K, V double buffered
+    static constexpr int SMEM_ELEMS_RAW = 2 * BUF;
     static constexpr int STAGE_ELEMS = NW * 32 * OW;
     static constexpr int SMEM_ELEMS = SMEM_ELEMS_RAW > STAGE_ELEMS ? SMEM_ELEMS_RAW : STAGE_ELEMS;
     // fp32 at D=128 needs more than 256 registers per lane (Q, dO and dQ^T in fp32)
@@ -308,7 +327,7 @@ struct DqCfg {
 template <typename T, int D, bool CAUSAL, bool DROPOUT>
 __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(const BwdParams p, const int n_qtiles) {
     using C = DqCfg<T, D>;
-    constexpr int BN = C::BN, KW = C::KW;
+    constexpr int BN = C::BN, KW = C::KW, TW = C::TW;
     __shared__ __attribute__((aligned(16))) T smem[C::SMEM_ELEMS];
 
     const int tid = threadIdx.x;
@@ -338,6 +357,7 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
     const int64_t si = ((int64_t)b * p.H + h) * p.Sq + qi;
     const float lse2 = qi < p.Sq ? p.lse[si] * kLog2e : INFINITY;
     const float del = qi < p.Sq ? p.delta[si] : 0.f;
+    wait_vmem();
     const float c = p.scale_log2;
     uint64_t row_ctr = 0;
     if (DROPOUT) row_ctr = p.offset + ((uint64_t)(b * p.H + h) * (uint64_t)p.Sq + (uint64_t)qi) * (uint64_t)p.Sk;
@@ -349,28 +369,46 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
     int kv_end = p.Sk;
     if (CAUSAL) kv_end = min(kv_end, min(q0 + C::BM, p.Sq));
     const int n_tiles = (kv_end + BN - 1) / BN;
+    int n_plain = min(n_tiles, p.Sk / BN);
+    if (CAUSAL) n_plain = min(n_plain, (q0 + 1) / BN);
 
     const T* kbase = (const T*)p.k + b * p.k_sb + hk * p.k_sh;
     const T* vbase = (const T*)p.v + b * p.v_sb + hk * p.v_sh;
-    TileStage<T, BN, D, C::NT> kst, vst;
-    T* Ks0 = smem;
-    T* Vs0 = smem + 2 * C::KTILE;
-    if (n_tiles > 0) {
-        kst.load(kbase, p.k_ss, p.Sk, tid);
-        vst.load(vbase, p.v_ss, p.Sk, tid);
-        kst.template store<KW>(Ks0, tid);
-        vst.template store<KW>(Vs0, tid);
-    }
-    for (int j = 0; j < n_tiles; ++j) {
-        const int k0 = j * BN;
-        if (j + 1 < n_tiles) {
-            kst.load(kbase + (int64_t)(k0 + BN) * p.k_ss, p.k_ss, p.Sk - (k0 + BN), tid);
-            vst.load(vbase + (int64_t)(k0 + BN) * p.v_ss, p.v_ss, p.Sk - (k0 + BN), tid);
+    // 16-bit types: waves 0-1 stage the K tile (rows and K^T), waves 2-3 the
+    // V tile; fp32 stages both with all threads.
+    using KStage = typename std::conditional<C::F32, TileStage<T, BN, D, C::NT>, Tile16<T, BN, D, C::NT / 2>>::type;
+    KStage kst, vst;
+    const bool stage_k = tid < C::NT / 2;  // wave-uniform
+    const int stid = tid & (C::NT / 2 - 1);
+    auto load_tile = [&](int k0) {
+        if constexpr (C::F32) {
+            kst.load(kbase + (int64_t)k0 * p.k_ss, p.k_ss, p.Sk - k0, tid);
+            vst.load(vbase + (int64_t)k0 * p.v_ss, p.v_ss, p.Sk - k0, tid);
+        } else {
+            if (stage_k) kst.load(kbase + (int64_t)k0 * p.k_ss, p.k_ss, p.Sk - k0, stid);
+            else kst.load(vbase + (int64_t)k0 * p.v_ss, p.v_ss, p.Sk - k0, stid);
         }
-        __syncthreads();
-        const T* Ks = Ks0 + (j & 1) * C::KTILE;
-        const T* Vs = Vs0 + (j & 1) * C::KTILE;
-        const bool active = !CAUSAL || k0 <= qw0 + 31;
+    };
+    auto store_tile = [&](int buf) {
+        T* base = smem + buf * C::BUF;
+        if constexpr (C::F32) {
+            kst.template store<KW>(base, tid);
+            vst.template store<KW>(base + C::KTILE, tid);
+        } else {
+            kst.template store_rows<KW>(base + (stage_k ? 0 : C::KTILE), stid);
+            if (stage_k) kst.template store_trans<TW>(base + 2 * C::KTILE, stid);
+        }
+    };
+
+    auto step = [&](int j, auto mask_tag) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const int k0 = j * BN;
+        if (j + 1 < n_tiles) load_tile(k0 + BN);
+        lds_barrier();
+        const T* Ks = smem + (j & 1) * C::BUF;
+        const T* Vs = Ks + C::KTILE;
+        const T* KT = Ks + 2 * C::KTILE;
+        const bool active = !MASK || !CAUSAL || k0 <= qw0 + 31;
         if (active) {
             f32x16 s = f32x16{}, dp = f32x16{};
             const T* krow = Ks + l32 * KW;
@@ -397,7 +435,7 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
                     dp = Elem<T>::mfma(av, __builtin_bit_cast(s16x8, doreg[kk]), dp);
                 }
             }
-            const bool need_mask = (k0 + BN > p.Sk) || (CAUSAL && k0 + BN - 1 > qw0);
+            const bool need_mask = MASK && ((k0 + BN > p.Sk) || (CAUSAL && k0 + BN - 1 > qw0));
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = k0 + 8 * (r >> 2) + 4 * hi + (r & 3);
@@ -418,8 +456,6 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
                     for (int i = 0; i < D / 32; ++i) dq[i] = mfma_f32(kr[32 * i], s[t], dq[i]);
                 }
             } else {
-                const int trow = 4 * hi + ((lane & 15) >> 2);
-                const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
                 for (int ks = 0; ks < BN / 16; ++ks) {
                     float ts[8];
@@ -428,20 +464,23 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
                     const s16x8 bs8 = pack8<T>(ts);
 #pragma unroll
                     for (int i = 0; i < D / 32; ++i) {
-                        const T* src = Ks + (16 * ks + trow) * KW + 32 * i + tcol;
-                        const s16x8 a = cat4(lds_read_tr16(src), lds_read_tr16(src + 8 * KW));
+                        const s16x8 a = *reinterpret_cast<const s16x8*>(KT + (32 * i + l32) * TW + 16 * ks + 8 * hi);
                         dq[i] = Elem<T>::mfma(a, bs8, dq[i]);
                     }
                 }
             }
         }
-        if (j + 1 < n_tiles) {
-            kst.template store<KW>(Ks0 + ((j + 1) & 1) * C::KTILE, tid);
-            vst.template store<KW>(Vs0 + ((j + 1) & 1) * C::KTILE, tid);
-        }
-    }
+        if (j + 1 < n_tiles) store_tile((j + 1) & 1);
+    };
 
-    __syncthreads();
+    if (n_tiles > 0) {
+        load_tile(0);
+        store_tile(0);
+    }
+    for (int j = 0; j < n_plain; ++j) step(j, std::false_type{});
+    for (int j = n_plain; j < n_tiles; ++j) step(j, std::true_type{});
+
+    lds_barrier();
     constexpr int OW = C::OW;
     T* Os = smem + w * 32 * OW;
 #pragma unroll
@@ -461,7 +500,7 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
                 *reinterpret_cast<s16x4*>(Os + l32 * OW + d) = v4;
             }
         }
-    __syncthreads();
+    lds_barrier();
     constexpr int EPC = 16 / sizeof(T);
     constexpr int CPR = D / EPC;
     T* gbase = (T*)p.dq + b * p.dq_sb + h * p.dq_sh;

@@ -73,6 +73,16 @@ __device__ inline float swap_halves(float x) { return __shfl_xor(x, 32, 64); }
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also fences global
+// memory, which on gfx9 (one counter for vector loads and stores) makes every
+// barrier wait for the in-flight prefetch of the next tile; the kernels never
+// communicate through global memory, so an LDS-scoped fence is sufficient.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ---------------------------------------------------------------------------
 // LDS access
 typedef __attribute__((address_space(3))) void lds_void;
@@ -129,8 +139,114 @@ __device__ inline int xcd_remap(int L, int N) {
 }
 
 // ---------------------------------------------------------------------------
+// Raw buffer view of rows [0, nvalid) of a row-strided [rows][D] slice: loads
+// at byte offsets past the last valid row return zeros (hardware range check),
+// which zero-fills tail tiles without any per-lane branch or select.  The
+// descriptor is rebuilt per tile (base advanced, record count reduced) so the
+// range check never depends on the scalar offset.
+template <typename T, int D>
+__device__ inline __amdgpu_buffer_rsrc_t row_buffer(const T* base, int64_t row_stride, int nvalid) {
+    const int64_t bytes = nvalid > 0 ? ((int64_t)(nvalid - 1) * row_stride + D) * (int64_t)sizeof(T) : 0;
+    // dword 3: DATA_FORMAT = 32 (untyped dword access), no swizzle, no stride
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
+}
+
+// Wait for all outstanding vector-memory loads.  Issued once after the
+// per-lane register operands (Q, dO, K, V rows, LSE, delta) are loaded, so the
+// compiler's wait tracking starts every tile loop with nothing pending and does
+// not re-wait for them (together with the next tile's prefetch) each iteration.
+__device__ inline void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+__device__ inline uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, int byte_offset) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 0));
+}
+
+// ---------------------------------------------------------------------------
+// Row permutation used by transposed LDS tiles.  The MFMA accumulator of
+// lane l holds rows {8(r/4) + 4(l/32) + r%4}; when those rows become the
+// contraction (k) index of a later product, the 8 k-values lane l supplies are
+// rows 16s + {4h .. 4h+3, 8+4h .. 8+4h+3} (h = l/32).  Storing row r at column
+// slot(r) = r with bits 2 and 3 swapped makes those 8 rows contiguous
+// (slots 16s + 8h .. 16s + 8h + 7), so one ds_read_b128 fetches the operand.
+__device__ inline int slot_of_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+
+// Global -> register -> LDS staging of a [R][D] tile of 16-bit elements.
+// Each thread owns units of 4 rows x 8 columns (four 16-byte loads).  Unit u
+// covers row group rg = 4 * (u / (4 * CG)) + u % 4 and column group
+// cg = (u / 4) % CG: consecutive lanes take consecutive row groups, so a wave
+// still reads whole rows per load instruction while the transposed stores of
+// neighbouring lanes land in one contiguous LDS row segment (2-way bank
+// conflicts at most instead of 8-way).  The tile can be
+// written to LDS row-major (store_rows) and/or transposed with the row
+// permutation above (store_trans: XT[d][slot_of_row(r)] = X[r][d], one
+// ds_write_b64 per column after a byte-permute of the four rows).
+template <typename T, int R, int D, int NT>
+struct Tile16 {
+    static_assert(sizeof(T) == 2, "16-bit elements only");
+    static_assert(R % 16 == 0 && D % 8 == 0, "tile shape");
+    static constexpr int CG = D / 8;
+    static constexpr int UNITS = (R / 4) * CG;
+    static constexpr int PER = (UNITS + NT - 1) / NT;
+    uint4 r[PER][4];
+
+    __device__ static inline int row_group(int u) { return 4 * ((u >> 2) / CG) + (u & 3); }
+    __device__ static inline int col_group(int u) { return (u >> 2) % CG; }
+
+    // Rows >= nvalid read as zeros (buffer range check); no branches or
+    // selects on the loaded data, so nothing forces an early wait on the loads.
+    __device__ inline void load(const T* __restrict__ base, int64_t row_stride, int nvalid, int tid) {
+        const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D>(base, row_stride, nvalid);
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int u = tid + i * NT;
+            if (UNITS % NT == 0 || u < UNITS) {
+                const int rg = row_group(u), cg = col_group(u);
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    r[i][k] = buffer_load16(rs, (int)(((4 * rg + k) * row_stride + 8 * cg) * (int64_t)sizeof(T)));
+            }
+        }
+    }
+    template <int W>
+    __device__ inline void store_rows(T* lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int u = tid + i * NT;
+            if (UNITS % NT == 0 || u < UNITS) {
+                const int rg = row_group(u), cg = col_group(u);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) *reinterpret_cast<uint4*>(lds + (4 * rg + k) * W + 8 * cg) = r[i][k];
+            }
+        }
+    }
+    template <int W>
+    __device__ inline void store_trans(T* ldsT, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int u = tid + i * NT;
+            if (UNITS % NT == 0 || u < UNITS) {
+                const int rg = row_group(u), cg = col_group(u);
+                const int s0 = slot_of_row(4 * rg);
+                const uint32_t* a = reinterpret_cast<const uint32_t*>(&r[i][0]);
+                const uint32_t* b = reinterpret_cast<const uint32_t*>(&r[i][1]);
+                const uint32_t* c = reinterpret_cast<const uint32_t*>(&r[i][2]);
+                const uint32_t* d = reinterpret_cast<const uint32_t*>(&r[i][3]);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+                    uint2 v;
+                    v.x = __builtin_amdgcn_perm(b[j >> 1], a[j >> 1], sel);  // rows 0,1 of column j
+                    v.y = __builtin_amdgcn_perm(d[j >> 1], c[j >> 1], sel);  // rows 2,3
+                    *reinterpret_cast<uint2*>(ldsT + (8 * cg + j) * W + s0) = v;
+                }
+            }
+        }
+    }
+};
+
+// ---------------------------------------------------------------------------
 // Global -> register -> LDS staging of a [ROWS][D] tile of T with 16-byte
-// chunks; rows >= nvalid are zero-filled.  LDS row stride LDSW elements.
+// chunks (LDS row stride LDSW elements); same tail handling as Tile16.
 template <typename T, int ROWS, int D, int NT>
 struct TileStage {
     static constexpr int EPC = 16 / sizeof(T);  // elements per 16-byte chunk
@@ -140,14 +256,13 @@ struct TileStage {
     uint4 r[PER];
 
     __device__ inline void load(const T* __restrict__ base, int64_t row_stride, int nvalid, int tid) {
+        const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D>(base, row_stride, nvalid);
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int c = tid + i * NT;
             const int row = c / CPR, col = c % CPR;
-            uint4 v = make_uint4(0u, 0u, 0u, 0u);
-            if ((TOTAL % NT == 0 || c < TOTAL) && row < nvalid)
-                v = *reinterpret_cast<const uint4*>(base + (int64_t)row * row_stride + col * EPC);
-            r[i] = v;
+            if (TOTAL % NT == 0 || c < TOTAL)
+                r[i] = buffer_load16(rs, (int)((row * row_stride + col * EPC) * (int64_t)sizeof(T)));
         }
     }
     template <int LDSW>

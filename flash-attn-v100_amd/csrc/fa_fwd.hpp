@@ -10,13 +10,17 @@
 //   * Q lives in registers for the whole KV loop (MFMA B operand).
 //   * K/V tiles stream through double-buffered LDS (one barrier per tile),
 //     loaded with 16-byte global loads issued a full tile ahead.
-//   * V^T operands come straight from row-major LDS via ds_read_b64_tr_b16.
+//   * V is written to LDS transposed (V^T[d][slot(key)], key order permuted to
+//     match the P accumulator layout), so PV operands are single ds_read_b128.
 //   * exp2 with scale*log2(e) folded into one FMA; the running max is only
 //     moved (and O rescaled) when it grows by more than 2^8, which is exact.
 //   * causal: KV tiles past the last query are never loaded; tiles past a
-//     wave's last query are skipped by that wave; only diagonal tiles mask.
+//     wave's last query are skipped by that wave; only diagonal and tail tiles
+//     run the masking variant of the tile step.
 //   * fp32 inputs use v_mfma_f32_32x32x2_f32 with fp32 P.
 #pragma once
+
+#include <type_traits>
 
 #include "fa_common.hpp"
 #include "fa_params.hpp"
@@ -28,13 +32,14 @@ struct FwdCfg {
     static constexpr bool F32 = Elem<T>::kF32;
     static constexpr int NW = 4;
     static constexpr int NT = 64 * NW;
-    static constexpr int BM = 32 * NW;           // queries per workgroup
-    static constexpr int BN = F32 ? 32 : 64;     // keys per tile
-    static constexpr int NB = BN / 32;           // 32-key blocks per tile
+    static constexpr int BM = 32 * NW;            // queries per workgroup
+    static constexpr int BN = F32 ? 32 : 64;      // keys per tile
+    static constexpr int NB = BN / 32;            // 32-key blocks per tile
     static constexpr int KW = D + (F32 ? 4 : 8);  // K row stride (elements)
-    static constexpr int VW = D + (F32 ? 8 : (D == 32 ? 64 : 32));  // V row stride
+    // V: fp32 keeps rows (stride D + 8); 16-bit types store V^T[d][slot(key)]
+    static constexpr int VW = F32 ? D + 8 : BN + 8;
     static constexpr int KTILE = BN * KW;
-    static constexpr int VTILE = BN * VW;
+    static constexpr int VTILE = F32 ? BN * VW : D * VW;
     static constexpr int OW = D + (F32 ? 4 : 8);  // output staging row stride
     static constexpr int SMEM_ELEMS = 2 * (KTILE + VTILE);
     static_assert(NW * 32 * OW <= SMEM_ELEMS, "O staging must fit in the K/V buffers");
@@ -64,6 +69,9 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     int kv_end = p.Sk;
     if (CAUSAL) kv_end = min(kv_end, min(q0 + C::BM, p.Sq));
     const int n_tiles = (kv_end + BN - 1) / BN;
+    // tiles before n_plain need no masking for any wave of the workgroup
+    int n_plain = min(n_tiles, p.Sk / BN);
+    if (CAUSAL) n_plain = min(n_plain, (q0 + 1) / BN);
 
     // ---- Q into registers (MFMA B operand) ----
     constexpr int QR = C::F32 ? D / 8 : D / 16;  // 16-byte registers per lane
@@ -77,6 +85,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
             qreg[i] = qi < p.Sq ? *reinterpret_cast<const uint4*>(qrow + d0) : make_uint4(0u, 0u, 0u, 0u);
         }
     }
+    wait_vmem();
 
     f32x16 o[D / 32];
 #pragma unroll
@@ -89,27 +98,34 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     uint64_t row_ctr = 0;
     if (DROPOUT) row_ctr = p.offset + ((uint64_t)(b * p.H + h) * (uint64_t)p.Sq + (uint64_t)qi) * (uint64_t)p.Sk;
 
-    TileStage<T, BN, D, C::NT> kst, vst;
     T* Ks0 = smem;
     T* Vs0 = smem + 2 * C::KTILE;
-    if (n_tiles > 0) {
-        kst.load(kbase, p.k_ss, p.Sk, tid);
-        vst.load(vbase, p.v_ss, p.Sk, tid);
-        kst.template store<KW>(Ks0, tid);
-        vst.template store<VW>(Vs0, tid);
-    }
-
-    for (int j = 0; j < n_tiles; ++j) {
-        const int k0 = j * BN;
-        if (j + 1 < n_tiles) {
-            kst.load(kbase + (int64_t)(k0 + BN) * p.k_ss, p.k_ss, p.Sk - (k0 + BN), tid);
-            vst.load(vbase + (int64_t)(k0 + BN) * p.v_ss, p.v_ss, p.Sk - (k0 + BN), tid);
+    using KStage = typename std::conditional<C::F32, TileStage<T, BN, D, C::NT>, Tile16<T, BN, D, C::NT>>::type;
+    KStage kst, vst;
+    auto load_tile = [&](int k0) {
+        kst.load(kbase + (int64_t)k0 * p.k_ss, p.k_ss, p.Sk - k0, tid);
+        vst.load(vbase + (int64_t)k0 * p.v_ss, p.v_ss, p.Sk - k0, tid);
+    };
+    auto store_tile = [&](int buf) {
+        if constexpr (C::F32) {
+            kst.template store<KW>(Ks0 + buf * C::KTILE, tid);
+            vst.template store<VW>(Vs0 + buf * C::VTILE, tid);
+        } else {
+            kst.template store_rows<KW>(Ks0 + buf * C::KTILE, tid);
+            vst.template store_trans<VW>(Vs0 + buf * C::VTILE, tid);
         }
-        __syncthreads();
+    };
+
+    // one KV tile; MASK selects the diagonal/tail variant
+    auto step = [&](int j, auto mask_tag) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const int k0 = j * BN;
+        if (j + 1 < n_tiles) load_tile(k0 + BN);
+        lds_barrier();
         const T* Ks = Ks0 + (j & 1) * C::KTILE;
         const T* Vs = Vs0 + (j & 1) * C::VTILE;
 
-        const bool active = !CAUSAL || k0 <= qw0 + 31;
+        const bool active = !MASK || !CAUSAL || k0 <= qw0 + 31;
         if (active) {
             // ---- S^T = K Q^T ----
             f32x16 s[NB];
@@ -133,16 +149,17 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
                     }
                 }
             }
-            // ---- masking (tails and the causal diagonal only) ----
-            const bool need_mask = (k0 + BN > p.Sk) || (CAUSAL && k0 + BN - 1 > qw0);
-            if (need_mask) {
+            if constexpr (MASK) {
+                const bool need = (k0 + BN > p.Sk) || (CAUSAL && k0 + BN - 1 > qw0);
+                if (need) {
 #pragma unroll
-                for (int blk = 0; blk < NB; ++blk)
+                    for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = k0 + 32 * blk + 8 * (r >> 2) + 4 * hi + (r & 3);
-                        if (key >= p.Sk || (CAUSAL && key > qi)) s[blk][r] = -INFINITY;
-                    }
+                        for (int r = 0; r < 16; ++r) {
+                            const int key = k0 + 32 * blk + 8 * (r >> 2) + 4 * hi + (r & 3);
+                            if (key >= p.Sk || (CAUSAL && key > qi)) s[blk][r] = -INFINITY;
+                        }
+                }
             }
             // ---- online softmax ----
             float mx = -INFINITY;
@@ -193,33 +210,29 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
                         for (int i = 0; i < D / 32; ++i) o[i] = mfma_f32(vrow[32 * i], s[blk][t], o[i]);
                     }
             } else {
-                s16x8 pk[BN / 16];
 #pragma unroll
                 for (int ks = 0; ks < BN / 16; ++ks) {
                     float tmp[8];
 #pragma unroll
                     for (int e = 0; e < 8; ++e) tmp[e] = s[ks >> 1][8 * (ks & 1) + e];
-                    pk[ks] = pack8<T>(tmp);
-                }
-                // source address of this lane for the transposing LDS read
-                const int trow = 4 * hi + ((lane & 15) >> 2);
-                const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-#pragma unroll
-                for (int ks = 0; ks < BN / 16; ++ks) {
+                    const s16x8 pk = pack8<T>(tmp);
 #pragma unroll
                     for (int i = 0; i < D / 32; ++i) {
-                        const T* src = Vs + (16 * ks + trow) * VW + 32 * i + tcol;
-                        const s16x8 a = cat4(lds_read_tr16(src), lds_read_tr16(src + 8 * VW));
-                        o[i] = Elem<T>::mfma(a, pk[ks], o[i]);
+                        const s16x8 a = *reinterpret_cast<const s16x8*>(Vs + (32 * i + l32) * VW + 16 * ks + 8 * hi);
+                        o[i] = Elem<T>::mfma(a, pk, o[i]);
                     }
                 }
             }
         }
-        if (j + 1 < n_tiles) {
-            kst.template store<KW>(Ks0 + ((j + 1) & 1) * C::KTILE, tid);
-            vst.template store<VW>(Vs0 + ((j + 1) & 1) * C::VTILE, tid);
-        }
+        if (j + 1 < n_tiles) store_tile((j + 1) & 1);
+    };
+
+    if (n_tiles > 0) {
+        load_tile(0);
+        store_tile(0);
     }
+    for (int j = 0; j < n_plain; ++j) step(j, std::false_type{});
+    for (int j = n_plain; j < n_tiles; ++j) step(j, std::true_type{});
 
     // ---- epilogue: normalise, LSE, stage O^T through LDS, coalesced store ----
     const float l_tot = l_run + swap_halves(l_run);
@@ -229,7 +242,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
         p.lse[si] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
         if (p.mx) p.mx[si] = m_raw * p.scale;
     }
-    __syncthreads();  // all waves done with the K/V buffers
+    lds_barrier();  // all waves done with the K/V buffers
     constexpr int OW = C::OW;
     T* Os = smem + w * 32 * OW;
 #pragma unroll
@@ -249,7 +262,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
                 *reinterpret_cast<s16x4*>(Os + l32 * OW + d) = v4;
             }
         }
-    __syncthreads();
+    lds_barrier();
     constexpr int EPC = 16 / sizeof(T);
     constexpr int CPR = D / EPC;
     T* obase = (T*)p.o + b * p.o_sb + h * p.o_sh;
