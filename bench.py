@@ -150,6 +150,19 @@ def _cpu_model():
     return None
 
 
+def _profiled_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` (read + write) from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload, already scaled
+    by the copy calibration; None if the kernel was not profiled."""
+    path = os.path.join(REPO, "profiles", "c3_bf16_causal_traffic.json")
+    try:
+        with open(path) as f:
+            k = json.load(f)["kernels"].get(kernel)
+    except (OSError, ValueError):
+        return None
+    return None if k is None else int(k["hbm_read_bytes"] + k["hbm_write_bytes"])
+
+
 def copy_calibration(gib: float = 1.0, reps: int = 5):
     """A plain device copy of known size, for scaling rocprofv3's FETCH_SIZE /
     WRITE_SIZE counters (KiB per dispatch) to bytes."""
@@ -193,15 +206,17 @@ def main():
     # (QK^T recompute, dO V^T, P^T dO, dS^T Q); dq = dS K (its S/dP recompute is extra work)
     algo = {"fwd_kernel": F, "dkdv_kernel": 2.0 * F, "dq_kernel": 0.5 * F}
     dom = max(kernels, key=kernels.get)
+    traffic = _profiled_traffic(dom)
     if dom in algo:
         ach = algo[dom] / (kernels[dom] * 1e-3) / 1e12
         roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None}
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                "algorithmic_flop_per_launch": algo[dom]}
     else:
         nbytes = 2 * B * S * H * D * 2 + 4 * B * H * S
         ach = nbytes / (kernels[dom] * 1e-3) / 1e9
         roof = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS,
-                "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None}
+                "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": traffic}
     out = {
         "metric": METRIC,
         "value": round(value, 2),

@@ -46,6 +46,15 @@ void split(const int64_t st[4], int64_t& sb, int64_t& ss, int64_t& sh) {
 
 int32_t status_of(hipError_t e) { return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH; }
 
+// The kernels address one (batch, head) slice of a tensor through a raw buffer
+// descriptor with a 32-bit byte range: rows [0, S) of the slice must span
+// less than 2^31 bytes.
+int32_t check_span(const int64_t st[4], int32_t S, int32_t D, int es) {
+    if (S <= 0) return FA_OK;
+    const int64_t span = ((int64_t)(S - 1) * st[1] + D) * es;
+    return span < (1LL << 31) ? FA_OK : FA_ERR_TOO_LARGE;
+}
+
 }  // namespace
 
 extern "C" {
@@ -86,6 +95,11 @@ int32_t fa_fwd_check(const fa_fwd_args* a) {
         return st;
     if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o)) return FA_ERR_ALIGN;
     if (((uintptr_t)a->lse & 3u) || ((uintptr_t)a->max_vals & 3u)) return FA_ERR_ALIGN;
+    if ((st = check_span(a->q_stride, a->seqlen_q, a->head_dim, es)) ||
+        (st = check_span(a->k_stride, a->seqlen_k, a->head_dim, es)) ||
+        (st = check_span(a->v_stride, a->seqlen_k, a->head_dim, es)) ||
+        (st = check_span(a->o_stride, a->seqlen_q, a->head_dim, es)))
+        return st;
     return FA_OK;
 }
 
@@ -154,6 +168,10 @@ int32_t fa_bwd_check(const fa_bwd_args* a, size_t ws_bytes) {
     for (int i = 0; i < 8; ++i)
         if (!aligned16(ptrs[i])) return FA_ERR_ALIGN;
     if ((uintptr_t)a->lse & 3u) return FA_ERR_ALIGN;
+    const int32_t rows[8] = {a->seqlen_q, a->seqlen_k, a->seqlen_k, a->seqlen_q,
+                             a->seqlen_q, a->seqlen_q, a->seqlen_k, a->seqlen_k};
+    for (int i = 0; i < 8; ++i)
+        if ((st = check_span(strides[i], rows[i], a->head_dim, es))) return st;
     const size_t need = fa_bwd_workspace_size(a);
     if (need > 0 && ws_bytes < need) return FA_ERR_WORKSPACE;
     return FA_OK;

@@ -43,7 +43,8 @@ extern "C" {
 #define FA_ERR_ALIGN -9       /* a tensor base pointer is not 16-byte aligned */
 #define FA_ERR_SCALE -10      /* scale not finite and > 0 */
 #define FA_ERR_LAUNCH -11     /* the HIP runtime rejected a kernel launch */
-#define FA_ERR_TOO_LARGE -12  /* a grid dimension or index would overflow */
+#define FA_ERR_TOO_LARGE -12  /* a grid dimension would overflow, or the rows of one
+                                 (batch, head) slice of a tensor span >= 2^31 bytes */
 
 /* Forward arguments.
  * Replaces the launcher flash_attention_forward_triton_enhanced

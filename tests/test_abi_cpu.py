@@ -146,6 +146,14 @@ def test_fwd_check_strides_and_alignment():
     assert _status(a) == CODES["FA_ERR_ALIGN"]
 
 
+def test_fwd_check_rejects_slices_beyond_buffer_range():
+    a, _keep = _cpu_fwd()
+    a.seqlen_k = 70000
+    a.k_stride[1] = 64 * 256  # rows of one head 32 KiB apart: 70000 rows span > 2 GiB
+    a.k_stride[0] = a.k_stride[1] * 70000
+    assert _status(a) == CODES["FA_ERR_TOO_LARGE"]
+
+
 def test_fwd_check_empty_problem_is_ok():
     a, _keep = _cpu_fwd(Sq=0)
     a.q = None
