@@ -49,9 +49,16 @@ int32_t status_of(hipError_t e) { return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH
 // The kernels address one (batch, head) slice of a tensor through a raw buffer
 // descriptor with a 32-bit byte range: rows [0, S) of the slice must span
 // less than 2^31 bytes.
+// Kernels address one (batch, head) slice through a 32-bit buffer range and
+// compute tile offsets for up to kTileRows rows past a tile's first row (rows
+// past the sequence are zero-filled by the range check), so the byte span of
+// max(S, kTileRows) rows must fit 31 bits.
+constexpr int32_t kTileRows = 256;
+
 int32_t check_span(const int64_t st[4], int32_t S, int32_t D, int es) {
     if (S <= 0) return FA_OK;
-    const int64_t span = ((int64_t)(S - 1) * st[1] + D) * es;
+    const int64_t rows = S > kTileRows ? S : kTileRows;
+    const int64_t span = ((rows - 1) * st[1] + D) * es;
     return span < (1LL << 31) ? FA_OK : FA_ERR_TOO_LARGE;
 }
 

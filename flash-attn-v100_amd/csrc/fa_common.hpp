@@ -144,9 +144,14 @@ __device__ inline int xcd_remap(int L, int N) {
 // which zero-fills tail tiles without any per-lane branch or select.  The
 // descriptor is rebuilt per tile (base advanced, record count reduced) so the
 // range check never depends on the scalar offset.
+//
+// The host rejects slices whose rows span 2^31 bytes or more, so for
+// 0 <= nvalid <= rows the byte count fits 32 bits; it is computed without a
+// branch (nvalid <= 0 gives 0) so that a tile load does not end a basic block.
 template <typename T, int D>
 __device__ inline __amdgpu_buffer_rsrc_t row_buffer(const T* base, int64_t row_stride, int nvalid) {
-    const int64_t bytes = nvalid > 0 ? ((int64_t)(nvalid - 1) * row_stride + D) * (int64_t)sizeof(T) : 0;
+    const int nv = max(nvalid, 0);
+    const int bytes = ((nv - 1) * (int)row_stride + D) * (int)sizeof(T) * min(nv, 1);
     // dword 3: DATA_FORMAT = 32 (untyped dword access), no swizzle, no stride
     return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
 }
@@ -171,26 +176,32 @@ __device__ inline uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, int byte_offset)
 __device__ inline int slot_of_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
 // Global -> register -> LDS staging of a [R][D] tile of 16-bit elements.
-// Each thread owns units of 4 rows x 8 columns (four 16-byte loads).  Unit u
-// covers row group rg = 4 * (u / (4 * CG)) + u % 4 and column group
-// cg = (u / 4) % CG: consecutive lanes take consecutive row groups, so a wave
-// still reads whole rows per load instruction while the transposed stores of
-// neighbouring lanes land in one contiguous LDS row segment (2-way bank
-// conflicts at most instead of 8-way).  The tile can be
-// written to LDS row-major (store_rows) and/or transposed with the row
+// Each thread owns units of 4 rows x 8 columns (four 16-byte loads) and can
+// write them to LDS row-major (store_rows) and/or transposed with the row
 // permutation above (store_trans: XT[d][slot_of_row(r)] = X[r][d], one
 // ds_write_b64 per column after a byte-permute of the four rows).
-template <typename T, int R, int D, int NT>
+//
+// Unit -> lane mapping (RG = R/4 row groups, CG = D/8 column groups):
+//  * ROWS_FAST = false: row group rg = 4 * (u / (4 * CG)) + u % 4, column
+//    group cg = (u / 4) % CG.  Each load instruction of a wave covers whole
+//    rows, and 16 consecutive lanes of a row store cover all 64 LDS banks.
+//  * ROWS_FAST = true (for store_trans): rg = u % RG, cg = u / RG.  One
+//    transposed store instruction then writes rows 8cg + j of only four
+//    column groups, at 16 distinct slot offsets each; with the other mapping
+//    the 16 column groups of one instruction write rows 8 apart, and rows 16
+//    apart share banks for every 16-byte-aligned row stride.
+template <typename T, int R, int D, int NT, bool ROWS_FAST = false>
 struct Tile16 {
     static_assert(sizeof(T) == 2, "16-bit elements only");
     static_assert(R % 16 == 0 && D % 8 == 0, "tile shape");
     static constexpr int CG = D / 8;
-    static constexpr int UNITS = (R / 4) * CG;
+    static constexpr int RG = R / 4;
+    static constexpr int UNITS = RG * CG;
     static constexpr int PER = (UNITS + NT - 1) / NT;
     uint4 r[PER][4];
 
-    __device__ static inline int row_group(int u) { return 4 * ((u >> 2) / CG) + (u & 3); }
-    __device__ static inline int col_group(int u) { return (u >> 2) % CG; }
+    __device__ static inline int row_group(int u) { return ROWS_FAST ? u % RG : 4 * ((u >> 2) / CG) + (u & 3); }
+    __device__ static inline int col_group(int u) { return ROWS_FAST ? u / RG : (u >> 2) % CG; }
 
     // Rows >= nvalid read as zeros (buffer range check); no branches or
     // selects on the loaded data, so nothing forces an early wait on the loads.
@@ -239,6 +250,63 @@ struct Tile16 {
                     v.y = __builtin_amdgcn_perm(d[j >> 1], c[j >> 1], sel);  // rows 2,3
                     *reinterpret_cast<uint2*>(ldsT + (8 * cg + j) * W + s0) = v;
                 }
+            }
+        }
+    }
+};
+
+// One 16-byte-per-lane global -> LDS load (buffer_load_dwordx4 ... lds): lane
+// l writes LDS bytes [16 l, 16 l + 16) past `lds`, which must be wave-uniform.
+// A function of its own: written directly in the kernel templates, the
+// builtin made the host pass emit launch stubs only for the first
+// instantiation of each kernel (the library then fails to load).
+template <typename T>
+__device__ inline void dma_load16(__amdgpu_buffer_rsrc_t rs, T* lds, int byte_offset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, byte_offset, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Direct global -> LDS copy of a [R][D] tile (buffer_load_dwordx4 ... lds):
+// no staging registers and no LDS store instructions.  The tile occupies LDS
+// rows of W elements (W - D of padding).  One wave instruction writes 64
+// consecutive 16-byte LDS chunks, lane l to chunk l (checked on gfx950), so
+// LDS chunk c of the tile is row c / CW, column chunk c % CW (CW = W * size /
+// 16); padding chunks load a copy of the row's last data chunk.  Instructions
+// are dealt round-robin to the NW waves of the workgroup.  Rows >= nvalid are
+// outside the buffer range and land as zeros.  The data is in LDS once the
+// issuing wave's vmcnt reaches zero; a workgroup barrier after that wait
+// publishes it to the other waves.
+template <typename T, int R, int D, int W, int NW>
+struct DmaTile {
+    static constexpr int EPC = 16 / (int)sizeof(T);
+    static constexpr int CD = D / EPC;
+    static constexpr int CW = W / EPC;
+    static_assert(D % EPC == 0 && W % EPC == 0 && W >= D, "16-byte chunked rows");
+    static constexpr int CHUNKS = R * CW;
+    static constexpr int NI = (CHUNKS + 63) / 64;
+    static constexpr int PER = (NI + NW - 1) / NW;
+    int off[PER];
+    int wave;
+
+    // wave_id must be wave-uniform (readfirstlane): it selects the LDS
+    // destination, which the hardware takes from a scalar register (M0).
+    __device__ inline void init(int64_t row_stride, int lane, int wave_id) {
+        wave = wave_id;
+#pragma unroll
+        for (int t = 0; t < PER; ++t) {
+            const int c = 64 * (wave + NW * t) + lane;
+            const int row = c / CW, col = min(c % CW, CD - 1);
+            off[t] = (row * (int)row_stride + col * EPC) * (int)sizeof(T);
+        }
+    }
+    __device__ inline void load(const T* base, int64_t row_stride, int nvalid, T* lds, int lane) const {
+        const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D>(base, row_stride, nvalid);
+#pragma unroll
+        for (int t = 0; t < PER; ++t) {
+            const int g = wave + NW * t;
+            if (NI % NW == 0 || g < NI) {
+                if (CHUNKS % 64 == 0 || 64 * g + lane < CHUNKS)
+                    dma_load16(rs, lds + 64 * g * EPC, off[t]);
             }
         }
     }

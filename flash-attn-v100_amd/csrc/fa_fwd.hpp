@@ -100,139 +100,221 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
 
     T* Ks0 = smem;
     T* Vs0 = smem + 2 * C::KTILE;
-    using KStage = typename std::conditional<C::F32, TileStage<T, BN, D, C::NT>, Tile16<T, BN, D, C::NT>>::type;
-    KStage kst, vst;
-    auto load_tile = [&](int k0) {
-        kst.load(kbase + (int64_t)k0 * p.k_ss, p.k_ss, p.Sk - k0, tid);
-        vst.load(vbase + (int64_t)k0 * p.v_ss, p.v_ss, p.Sk - k0, tid);
+    // K tiles (and fp32 V tiles, kept row-major) go global -> LDS directly;
+    // 16-bit V tiles are staged through registers and stored transposed.
+    // Loads past the last key read as zeros (buffer range check), so the
+    // pipeline below issues them unconditionally; such tiles are never used.
+    const int wv = __builtin_amdgcn_readfirstlane(w);
+    DmaTile<T, BN, D, KW, C::NW> kdma;
+    kdma.init(p.k_ss, lane, wv);
+    auto dma_k = [&](int j, int slot) {
+        kdma.load(kbase + (int64_t)(j * BN) * p.k_ss, p.k_ss, p.Sk - j * BN, Ks0 + slot * C::KTILE, lane);
     };
-    auto store_tile = [&](int buf) {
-        if constexpr (C::F32) {
-            kst.template store<KW>(Ks0 + buf * C::KTILE, tid);
-            vst.template store<VW>(Vs0 + buf * C::VTILE, tid);
-        } else {
-            kst.template store_rows<KW>(Ks0 + buf * C::KTILE, tid);
-            vst.template store_trans<VW>(Vs0 + buf * C::VTILE, tid);
+    using VStage = typename std::conditional<C::F32, DmaTile<T, BN, D, VW, C::NW>, Tile16<T, BN, D, C::NT, true>>::type;
+    VStage vst;
+    if constexpr (C::F32) vst.init(p.v_ss, lane, wv);
+    // 16-bit: load V(j) into registers; fp32: copy V(j) into V slot `slot`
+    auto load_v = [&](int j, int slot) {
+        if constexpr (C::F32) vst.load(vbase + (int64_t)(j * BN) * p.v_ss, p.v_ss, p.Sk - j * BN, Vs0 + slot * C::VTILE, lane);
+        else vst.load(vbase + (int64_t)(j * BN) * p.v_ss, p.v_ss, p.Sk - j * BN, tid);
+    };
+    auto store_v = [&](int slot) {
+        if constexpr (!C::F32) vst.template store_trans<VW>(Vs0 + slot * C::VTILE, tid);
+    };
+
+    // ---- S^T = K Q^T for one key tile ----
+    auto qk = [&](const T* Ks, f32x16 (&s)[NB]) {
+#pragma unroll
+        for (int blk = 0; blk < NB; ++blk) {
+            s[blk] = f32x16{};
+            const T* krow = Ks + (32 * blk + l32) * KW;
+            if constexpr (C::F32) {
+#pragma unroll
+                for (int i = 0; i < QR; ++i) {
+                    const f32x4 a = *reinterpret_cast<const f32x4*>(krow + hi * (D / 2) + 4 * i);
+                    const f32x4 bq = __builtin_bit_cast(f32x4, qreg[i]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) s[blk] = mfma_f32(a[e], bq[e], s[blk]);
+                }
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < QR; ++kk) {
+                    const s16x8 a = *reinterpret_cast<const s16x8*>(krow + 16 * kk + 8 * hi);
+                    s[blk] = Elem<T>::mfma(a, __builtin_bit_cast(s16x8, qreg[kk]), s[blk]);
+                }
+            }
         }
     };
-
-    // one KV tile; MASK selects the diagonal/tail variant
-    auto step = [&](int j, auto mask_tag) {
-        constexpr bool MASK = decltype(mask_tag)::value;
-        const int k0 = j * BN;
-        if (j + 1 < n_tiles) load_tile(k0 + BN);
-        lds_barrier();
-        const T* Ks = Ks0 + (j & 1) * C::KTILE;
-        const T* Vs = Vs0 + (j & 1) * C::VTILE;
-
-        const bool active = !MASK || !CAUSAL || k0 <= qw0 + 31;
-        if (active) {
-            // ---- S^T = K Q^T ----
-            f32x16 s[NB];
-#pragma unroll
-            for (int blk = 0; blk < NB; ++blk) {
-                s[blk] = f32x16{};
-                const T* krow = Ks + (32 * blk + l32) * KW;
-                if constexpr (C::F32) {
-#pragma unroll
-                    for (int i = 0; i < QR; ++i) {
-                        const f32x4 a = *reinterpret_cast<const f32x4*>(krow + hi * (D / 2) + 4 * i);
-                        const f32x4 bq = __builtin_bit_cast(f32x4, qreg[i]);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) s[blk] = mfma_f32(a[e], bq[e], s[blk]);
-                    }
-                } else {
-#pragma unroll
-                    for (int kk = 0; kk < QR; ++kk) {
-                        const s16x8 a = *reinterpret_cast<const s16x8*>(krow + 16 * kk + 8 * hi);
-                        s[blk] = Elem<T>::mfma(a, __builtin_bit_cast(s16x8, qreg[kk]), s[blk]);
-                    }
-                }
-            }
-            if constexpr (MASK) {
-                const bool need = (k0 + BN > p.Sk) || (CAUSAL && k0 + BN - 1 > qw0);
-                if (need) {
-#pragma unroll
-                    for (int blk = 0; blk < NB; ++blk)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int key = k0 + 32 * blk + 8 * (r >> 2) + 4 * hi + (r & 3);
-                            if (key >= p.Sk || (CAUSAL && key > qi)) s[blk][r] = -INFINITY;
-                        }
-                }
-            }
-            // ---- online softmax ----
-            float mx = -INFINITY;
-#pragma unroll
-            for (int blk = 0; blk < NB; ++blk)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[blk][r]);
-            mx = fmaxf(mx, swap_halves(mx));
-            m_raw = fmaxf(m_raw, mx);
-            const float m_new = fmaxf(m_run, mx * c);
-            if (__ballot(m_new > m_run + 8.0f) != 0ull) {
-                const float alpha = fast_exp2(m_run - m_new);
-                l_run *= alpha;
-#pragma unroll
-                for (int i = 0; i < D / 32; ++i)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
-                m_run = m_new;
-            }
-            float psum = 0.f;
+    // keys past Sk, and (causal) keys after the lane's query, to -inf
+    auto mask = [&](f32x16 (&s)[NB], int k0) {
+        const bool need = (k0 + BN > p.Sk) || (CAUSAL && k0 + BN - 1 > qw0);
+        if (need) {
 #pragma unroll
             for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const float pv = fast_exp2(__builtin_fmaf(s[blk][r], c, -m_run));
-                    psum += pv;
-                    s[blk][r] = pv;
+                    const int key = k0 + 32 * blk + 8 * (r >> 2) + 4 * hi + (r & 3);
+                    if (key >= p.Sk || (CAUSAL && key > qi)) s[blk][r] = -INFINITY;
                 }
-            l_run += psum;
-            if (DROPOUT) {
+        }
+    };
+    // running max; O and l are rescaled (lazily: only when the max grows by
+    // more than 2^8) before the tile's probabilities are added
+    auto update_max = [&](const f32x16 (&s)[NB]) {
+        float mx = -INFINITY;
 #pragma unroll
-                for (int blk = 0; blk < NB; ++blk)
+        for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = k0 + 32 * blk + 8 * (r >> 2) + 4 * hi + (r & 3);
-                        const float u = philox_uniform(p.seed, row_ctr + (uint64_t)key);
-                        if (!(u > p.dropout_p)) s[blk][r] = 0.f;
-                    }
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[blk][r]);
+        mx = fmaxf(mx, swap_halves(mx));
+        m_raw = fmaxf(m_raw, mx);
+        const float m_new = fmaxf(m_run, mx * c);
+        if (__ballot(m_new > m_run + 8.0f) != 0ull) {
+            const float alpha = fast_exp2(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+            m_run = m_new;
+        }
+    };
+    // P = exp2(S * scale * log2 e - m), row sums, dropout; 16-bit types pack P
+    constexpr int NPK = C::F32 ? 1 : BN / 16;
+    auto softmax = [&](f32x16 (&s)[NB], s16x8 (&pk)[NPK], int k0) {
+        float psum = 0.f;
+#pragma unroll
+        for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float pv = fast_exp2(__builtin_fmaf(s[blk][r], c, -m_run));
+                psum += pv;
+                s[blk][r] = pv;
             }
-            // ---- O^T += V^T P^T ----
-            if constexpr (C::F32) {
+        l_run += psum;
+        if (DROPOUT) {
 #pragma unroll
-                for (int blk = 0; blk < NB; ++blk)
+            for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
-                    for (int t = 0; t < 16; ++t) {
-                        const T* vrow = Vs + (32 * blk + 8 * (t >> 2) + 4 * hi + (t & 3)) * VW + l32;
-#pragma unroll
-                        for (int i = 0; i < D / 32; ++i) o[i] = mfma_f32(vrow[32 * i], s[blk][t], o[i]);
-                    }
-            } else {
-#pragma unroll
-                for (int ks = 0; ks < BN / 16; ++ks) {
-                    float tmp[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) tmp[e] = s[ks >> 1][8 * (ks & 1) + e];
-                    const s16x8 pk = pack8<T>(tmp);
-#pragma unroll
-                    for (int i = 0; i < D / 32; ++i) {
-                        const s16x8 a = *reinterpret_cast<const s16x8*>(Vs + (32 * i + l32) * VW + 16 * ks + 8 * hi);
-                        o[i] = Elem<T>::mfma(a, pk, o[i]);
-                    }
+                for (int r = 0; r < 16; ++r) {
+                    const int key = k0 + 32 * blk + 8 * (r >> 2) + 4 * hi + (r & 3);
+                    const float u = philox_uniform(p.seed, row_ctr + (uint64_t)key);
+                    if (!(u > p.dropout_p)) s[blk][r] = 0.f;
                 }
+        }
+        if constexpr (!C::F32) {
+#pragma unroll
+            for (int ks = 0; ks < BN / 16; ++ks) {
+                float tmp[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) tmp[e] = s[ks >> 1][8 * (ks & 1) + e];
+                pk[ks] = pack8<T>(tmp);
             }
         }
-        if (j + 1 < n_tiles) store_tile((j + 1) & 1);
+    };
+    // ---- O^T += V^T P^T ----
+    auto pv = [&](const T* Vs, const f32x16 (&s)[NB], const s16x8 (&pk)[NPK]) {
+        if constexpr (C::F32) {
+#pragma unroll
+            for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    const T* vrow = Vs + (32 * blk + 8 * (t >> 2) + 4 * hi + (t & 3)) * VW + l32;
+#pragma unroll
+                    for (int i = 0; i < D / 32; ++i) o[i] = mfma_f32(vrow[32 * i], s[blk][t], o[i]);
+                }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < BN / 16; ++ks)
+#pragma unroll
+                for (int i = 0; i < D / 32; ++i) {
+                    const s16x8 a = *reinterpret_cast<const s16x8*>(Vs + (32 * i + l32) * VW + 16 * ks + 8 * hi);
+                    o[i] = Elem<T>::mfma(a, pk[ks], o[i]);
+                }
+        }
     };
 
+    // Software pipeline over key tiles.  Iteration j issues the MFMAs of
+    // S(j+1) together with the softmax of S(j) (VALU) and the LDS store of the
+    // staged V tile, then P(j) V(j) together with the max of S(j+1) and the
+    // loads of the next tiles, so that the matrix pipe, the VALU, LDS and the
+    // memory pipe overlap inside one wave.
+    //
+    // LDS holds two K slots and two V slots.  Iteration j reads K(j+1) from
+    // K slot (j+1)&1 and V(j) from V slot j&1.  It copies K(j+2) into K slot
+    // j&1 and (16-bit) stores the registers holding V(j+1) into V slot
+    // (j+1)&1 -- both slots were last read in iteration j-1, which every wave
+    // finished before the barrier that opens iteration j -- and then loads
+    // V(j+2) into the registers (fp32: copies V(j+1) into its slot directly).
+    // Direct-to-LDS copies complete when the issuing wave's vmcnt drains, so
+    // every barrier that publishes tiles is preceded by a wait for all of the
+    // wave's outstanding loads (sync_tiles); the compiler only orders them
+    // against the wave's own LDS reads.
+    //
+    // Waves whose queries all precede a key tile (causal) skip it; tiles
+    // before n_plain need no mask for any wave of the workgroup.
+    int n_w = n_tiles;
+    if (CAUSAL) n_w = min(n_tiles, (qw0 + 31) / BN + 1);
+    f32x16 sa[NB], sb[NB];
+    s16x8 pk[NPK];
+
+    auto sync_tiles = [&]() {
+        wait_vmem();
+        lds_barrier();
+    };
     if (n_tiles > 0) {
-        load_tile(0);
-        store_tile(0);
+        dma_k(0, 0);
+        dma_k(1, 1);
+        load_v(0, 0);
+        store_v(0);
+        if constexpr (!C::F32) load_v(1, 1);
     }
-    for (int j = 0; j < n_plain; ++j) step(j, std::false_type{});
-    for (int j = n_plain; j < n_tiles; ++j) step(j, std::true_type{});
+    sync_tiles();
+    if (n_w > 0) {
+        qk(Ks0, sa);
+        if (n_plain == 0) mask(sa, 0);
+        update_max(sa);
+    }
+
+    auto iter = [&](int j, f32x16 (&sc)[NB], f32x16 (&sn)[NB], auto mask_tag) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        sync_tiles();
+        dma_k(j + 2, j & 1);
+        if constexpr (C::F32) load_v(j + 1, (j + 1) & 1);
+        const bool act = !MASK || j < n_w;
+        const bool next = !MASK || j + 1 < n_w;
+        if (act) {
+            if (next) qk(Ks0 + ((j + 1) & 1) * C::KTILE, sn);
+            softmax(sc, pk, j * BN);
+        }
+        store_v((j + 1) & 1);
+        if constexpr (!C::F32) load_v(j + 2, 0);
+        if (act) pv(Vs0 + (j & 1) * C::VTILE, sc, pk);
+        if (act && next) {
+            if (MASK) mask(sn, (j + 1) * BN);
+            update_max(sn);
+        }
+    };
+
+    // plain iterations: S(j) and S(j+1) both unmasked (unrolled by two so
+    // the score registers swap roles without copies)
+    const int n_pipe = n_plain - 1;
+    int j = 0;
+    for (; j + 1 < n_pipe; j += 2) {
+        iter(j, sa, sb, std::false_type{});
+        iter(j + 1, sb, sa, std::false_type{});
+    }
+    if (j < n_pipe) {
+        iter(j, sa, sb, std::false_type{});
+        ++j;
+#pragma unroll
+        for (int blk = 0; blk < NB; ++blk) sa[blk] = sb[blk];
+    }
+    for (; j + 1 < n_tiles; j += 2) {
+        iter(j, sa, sb, std::true_type{});
+        iter(j + 1, sb, sa, std::true_type{});
+    }
+    if (j < n_tiles) iter(j, sa, sb, std::true_type{});
 
     // ---- epilogue: normalise, LSE, stage O^T through LDS, coalesced store ----
     const float l_tot = l_run + swap_halves(l_run);
@@ -242,7 +324,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
         p.lse[si] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
         if (p.mx) p.mx[si] = m_raw * p.scale;
     }
-    lds_barrier();  // all waves done with the K/V buffers
+    sync_tiles();  // all waves done with the K/V buffers and no copy still in flight
     constexpr int OW = C::OW;
     T* Os = smem + w * 32 * OW;
 #pragma unroll

@@ -43,8 +43,9 @@ extern "C" {
 #define FA_ERR_ALIGN -9       /* a tensor base pointer is not 16-byte aligned */
 #define FA_ERR_SCALE -10      /* scale not finite and > 0 */
 #define FA_ERR_LAUNCH -11     /* the HIP runtime rejected a kernel launch */
-#define FA_ERR_TOO_LARGE -12  /* a grid dimension would overflow, or the rows of one
-                                 (batch, head) slice of a tensor span >= 2^31 bytes */
+#define FA_ERR_TOO_LARGE -12  /* a grid dimension would overflow, or max(S, 256) rows
+                                 of one (batch, head) slice of a tensor span >= 2^31
+                                 bytes (S = its sequence length) */
 
 /* Forward arguments.
  * Replaces the launcher flash_attention_forward_triton_enhanced

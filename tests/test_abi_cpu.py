@@ -40,6 +40,13 @@ def test_exports_every_declared_function():
         assert hasattr(lib, name)
 
 
+def test_no_undefined_kernel_symbols():
+    # every kernel launch stub the host code references is defined in the library
+    out = subprocess.run(["nm", "-D", "--undefined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    missing = [ln.split()[-1] for ln in out.splitlines() if "_ZN2fa" in ln]
+    assert not missing, missing
+
+
 def _c_layout():
     src = r"""
 #include <stdio.h>
