@@ -27,7 +27,9 @@
 namespace fa {
 
 // ---------------------------------------------------------------------------
-// delta = rowsum(dO * O)
+// delta = rowsum(dO * O) and LSE * log2(e) into the padded workspace rows;
+// padding rows (Sq <= i < sq_pad) get delta = 0 and LSE * log2(e) = +inf, so
+// a query tile that reads them gets P = 0 without a range check.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void delta_kernel(const BwdParams p) {
     constexpr int EPC = 16 / sizeof(T);
@@ -36,14 +38,16 @@ __global__ __launch_bounds__(256) void delta_kernel(const BwdParams p) {
     const int tid = threadIdx.x;
     const int64_t row = (int64_t)blockIdx.x * RPB + tid / LPR;
     const int part = tid % LPR;
-    const int64_t nrows = (int64_t)p.B * p.Sq * p.H;
+    const int64_t nrows = (int64_t)p.B * p.sq_pad * p.H;
     float acc = 0.f;
     int b = 0, i = 0, h = 0;
     if (row < nrows) {
         h = (int)(row % p.H);
         const int64_t bi = row / p.H;
-        i = (int)(bi % p.Sq);
-        b = (int)(bi / p.Sq);
+        i = (int)(bi % p.sq_pad);
+        b = (int)(bi / p.sq_pad);
+    }
+    if (row < nrows && i < p.Sq) {
         const T* orow = (const T*)p.o + b * p.o_sb + (int64_t)i * p.o_ss + h * p.o_sh + part * EPC;
         const T* drow = (const T*)p.dout + b * p.do_sb + (int64_t)i * p.do_ss + h * p.do_sh + part * EPC;
         const uint4 ov = *reinterpret_cast<const uint4*>(orow);
@@ -60,7 +64,11 @@ __global__ __launch_bounds__(256) void delta_kernel(const BwdParams p) {
     }
 #pragma unroll
     for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if (row < nrows && part == 0) p.delta[((int64_t)b * p.H + h) * p.Sq + i] = acc;
+    if (row < nrows && part == 0) {
+        const int64_t wi = ((int64_t)b * p.H + h) * p.sq_pad + i;
+        p.delta[wi] = acc;
+        p.lse2[wi] = i < p.Sq ? p.lse[((int64_t)b * p.H + h) * p.Sq + i] * kLog2e : INFINITY;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -76,12 +84,14 @@ struct DkdvCfg {
     // in the 256-byte bank window
     static constexpr int RW = D + (F32 ? 4 : (D == 64 ? 8 : 24));
     static constexpr int QTILE = BQ * RW;
-    // per buffer: Q rows, dO rows, then lse2[BQ] and delta[BQ] as floats
+    // per buffer: Q rows, dO rows, then LSE * log2 e [BQ] and delta [BQ] as floats
     static constexpr int BUF_BYTES = 2 * QTILE * (int)sizeof(T) + 2 * BQ * 4;
+    static constexpr int NBUF = 3;                  // tiles t, t+1 read while t+2 lands
     static constexpr int OW = D + (F32 ? 4 : 8);    // output staging stride
-    static constexpr int SMEM_BYTES_RAW = 2 * BUF_BYTES;
+    static constexpr int SMEM_BYTES_RAW = NBUF * BUF_BYTES;
     static constexpr int STAGE_BYTES = NW * 32 * OW * (int)sizeof(T);
     static constexpr int SMEM_BYTES = SMEM_BYTES_RAW > STAGE_BYTES ? SMEM_BYTES_RAW : STAGE_BYTES;
+    static_assert(BUF_BYTES % 16 == 0, "16-byte aligned buffers");
 };
 
 template <typename T, int D, bool CAUSAL, bool DROPOUT>
@@ -91,7 +101,8 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
     __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6, l32 = lane & 31, hi = lane >> 5;
+    // wave index as a scalar: loop bounds derived from it stay wave-uniform
+    const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
     const int L = xcd_remap(blockIdx.x, gridDim.x);
     const int bhk = L / n_ktiles;
     const int kt = L - bhk * n_ktiles;
@@ -121,145 +132,188 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
     for (int i = 0; i < D / 32; ++i) { dk[i] = f32x16{}; dv[i] = f32x16{}; }
     const float c = p.scale_log2;
 
-    // query tiles: causal needs queries >= k0 only; the first NMASK of them
-    // (per head) cross the key block and run the masking variant
+    // query tiles: causal needs queries >= k0 only; per query head of the
+    // group, the first tiles cross this wave's keys and are masked
     const int qt_begin = CAUSAL ? (k0 / BQ) : 0;
     const int qt_end = (p.Sq + BQ - 1) / BQ;
     const int nq = qt_end > qt_begin ? qt_end - qt_begin : 0;
     const int total = nq * p.group;  // (head in group) x (query tile)
+    const int n_mask = CAUSAL ? min(nq, max(0, (kw0 + 31 + BQ - 1) / BQ - qt_begin)) : 0;
 
-    TileStage<T, BQ, D, C::NT> qst, dost;
-    float lse_r = 0.f, del_r = 0.f;  // staged by threads tid < BQ
+    // ---- tiles: Q, dO rows and the LSE / delta rows, global -> LDS directly ----
+    const int wv = __builtin_amdgcn_readfirstlane(w);
+    DmaTile<T, BQ, D, RW, C::NW> qdma, ddma;
+    DmaTile<float, 1, BQ, BQ, C::NW> ldma;
+    qdma.init(p.q_ss, lane, wv);
+    ddma.init(p.do_ss, lane, wv);
+    ldma.init(BQ, lane, wv);
     auto buf = [&](int s) -> char* { return smem + s * C::BUF_BYTES; };
-    auto issue = [&](int it) {
-        const int hh = hk * p.group + it / nq;
-        const int qb0 = (qt_begin + it % nq) * BQ;
-        const T* qb = (const T*)p.q + b * p.q_sb + (int64_t)qb0 * p.q_ss + hh * p.q_sh;
-        const T* db = (const T*)p.dout + b * p.do_sb + (int64_t)qb0 * p.do_ss + hh * p.do_sh;
-        qst.load(qb, p.q_ss, p.Sq - qb0, tid);
-        dost.load(db, p.do_ss, p.Sq - qb0, tid);
-        if (tid < BQ) {
-            const int q = qb0 + tid;
-            const int64_t si = ((int64_t)b * p.H + hh) * p.Sq + q;
-            lse_r = q < p.Sq ? p.lse[si] * kLog2e : INFINITY;  // tail queries: P = 0
-            del_r = q < p.Sq ? p.delta[si] : 0.f;
-        }
-    };
-    auto commit = [&](int s) {
+    auto tile_head = [&](int it) { return hk * p.group + it / nq; };
+    auto tile_q0 = [&](int it) { return (qt_begin + it % nq) * BQ; };
+    auto issue = [&](int it, int s) FA_INLINE {
+        const int hh = tile_head(it), qb0 = tile_q0(it);
         char* bp = buf(s);
-        qst.template store<RW>((T*)bp, tid);
-        dost.template store<RW>((T*)bp + C::QTILE, tid);
+        qdma.load((const T*)p.q + b * p.q_sb + (int64_t)qb0 * p.q_ss + hh * p.q_sh, p.q_ss, p.Sq - qb0, (T*)bp, lane);
+        ddma.load((const T*)p.dout + b * p.do_sb + (int64_t)qb0 * p.do_ss + hh * p.do_sh, p.do_ss, p.Sq - qb0,
+                  (T*)bp + C::QTILE, lane);
+        const int64_t wrow = ((int64_t)b * p.H + hh) * p.sq_pad + qb0;  // qb0 + BQ <= sq_pad
         float* f = (float*)(bp + 2 * C::QTILE * sizeof(T));
-        if (tid < BQ) { f[tid] = lse_r; f[BQ + tid] = del_r; }
+        ldma.load(p.lse2 + wrow, BQ, 1, f, lane);
+        ldma.load(p.delta + wrow, BQ, 1, f + BQ, lane);
+    };
+    // direct-to-LDS copies complete when the issuing wave's vmcnt drains
+    auto sync_tiles = [&]() {
+        wait_vmem();
+        lds_barrier();
     };
 
-    auto step = [&](int it, auto mask_tag) {
-        constexpr bool MASK = decltype(mask_tag)::value;
-        if (it + 1 < total) issue(it + 1);
-        lds_barrier();
-        const char* bp = buf(it & 1);
-        const T* Qs = (const T*)bp;
+    // ---- S = Q K^T and dP = dO V^T for the tile in buffer s (C[q][key]) ----
+    auto sdp = [&](int s, f32x16& sc, f32x16& dpc) FA_INLINE {
+        const T* Qs = (const T*)buf(s);
         const T* Ds = Qs + C::QTILE;
-        const float* lse2 = (const float*)(bp + 2 * C::QTILE * sizeof(T));
-        const float* dels = lse2 + BQ;
-        const int hh = hk * p.group + it / nq;
-        const int qb0 = (qt_begin + it % nq) * BQ;
-
-        const bool active = (!MASK || !CAUSAL || qb0 + BQ - 1 >= kw0) && kw0 < p.Sk;
-        if (active) {
-            // ---- S = Q K^T and dP = dO V^T (C[q][key]) ----
-            f32x16 s = f32x16{}, dp = f32x16{};
-            const T* qrow = Qs + l32 * RW;
-            const T* drow = Ds + l32 * RW;
-            if constexpr (C::F32) {
+        sc = f32x16{};
+        dpc = f32x16{};
+        const T* qrow = Qs + l32 * RW;
+        const T* drow = Ds + l32 * RW;
+        if constexpr (C::F32) {
 #pragma unroll
-                for (int i = 0; i < KR; ++i) {
-                    const f32x4 aq = *reinterpret_cast<const f32x4*>(qrow + hi * (D / 2) + 4 * i);
-                    const f32x4 ad = *reinterpret_cast<const f32x4*>(drow + hi * (D / 2) + 4 * i);
-                    const f32x4 bk = __builtin_bit_cast(f32x4, kreg[i]);
-                    const f32x4 bv = __builtin_bit_cast(f32x4, vreg[i]);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        s = mfma_f32(aq[e], bk[e], s);
-                        dp = mfma_f32(ad[e], bv[e], dp);
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int kk = 0; kk < KR; ++kk) {
-                    const s16x8 aq = *reinterpret_cast<const s16x8*>(qrow + 16 * kk + 8 * hi);
-                    const s16x8 ad = *reinterpret_cast<const s16x8*>(drow + 16 * kk + 8 * hi);
-                    s = Elem<T>::mfma(aq, __builtin_bit_cast(s16x8, kreg[kk]), s);
-                    dp = Elem<T>::mfma(ad, __builtin_bit_cast(s16x8, vreg[kk]), dp);
-                }
-            }
-            // ---- P, dS ----
-            const bool need_mask = MASK && CAUSAL && qb0 < kw0 + 31;
-            uint64_t col_ctr = 0;
-            if (DROPOUT) col_ctr = p.offset + (uint64_t)(b * p.H + hh) * (uint64_t)p.Sq * (uint64_t)p.Sk + (uint64_t)kj;
-            float pd[16];
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse2 + 8 * g + 4 * hi);
-                const f32x4 d4 = *reinterpret_cast<const f32x4*>(dels + 8 * g + 4 * hi);
+            for (int i = 0; i < KR; ++i) {
+                const f32x4 aq = *reinterpret_cast<const f32x4*>(qrow + hi * (D / 2) + 4 * i);
+                const f32x4 ad = *reinterpret_cast<const f32x4*>(drow + hi * (D / 2) + 4 * i);
+                const f32x4 bk = __builtin_bit_cast(f32x4, kreg[i]);
+                const f32x4 bv = __builtin_bit_cast(f32x4, vreg[i]);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int r = 4 * g + e;
-                    const int q = qb0 + 8 * g + 4 * hi + e;
-                    float pv = fast_exp2(__builtin_fmaf(s[r], c, -l4[e]));
-                    if (need_mask && q < kj) pv = 0.f;
-                    float dpv = dp[r];
-                    float pdv = pv;
-                    if (DROPOUT) {
-                        const float u = philox_uniform(p.seed, col_ctr + (uint64_t)q * (uint64_t)p.Sk);
-                        const float z = u > p.dropout_p ? p.rp : 0.f;
-                        dpv *= z;
-                        pdv *= z;
-                    }
-                    pd[r] = pdv;
-                    s[r] = pv * (dpv - d4[e]);  // dS (scale applied at the end)
+                    sc = mfma_f32(aq[e], bk[e], sc);
+                    dpc = mfma_f32(ad[e], bv[e], dpc);
                 }
             }
-            // ---- dV^T += dO^T P,  dK^T += Q^T dS ----
-            if constexpr (C::F32) {
+        } else {
 #pragma unroll
-                for (int t = 0; t < 16; ++t) {
-                    const int qr = 8 * (t >> 2) + 4 * hi + (t & 3);
-#pragma unroll
-                    for (int i = 0; i < D / 32; ++i) {
-                        dv[i] = mfma_f32(Ds[qr * RW + 32 * i + l32], pd[t], dv[i]);
-                        dk[i] = mfma_f32(Qs[qr * RW + 32 * i + l32], s[t], dk[i]);
-                    }
-                }
-            } else {
-                // dO^T / Q^T operands straight from the row-major tiles
-                const int trow = 4 * hi + ((lane & 15) >> 2);
-                const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-#pragma unroll
-                for (int ks = 0; ks < BQ / 16; ++ks) {
-                    float tp[8], ts[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) { tp[e] = pd[8 * ks + e]; ts[e] = s[8 * ks + e]; }
-                    const s16x8 bp8 = pack8<T>(tp);
-                    const s16x8 bs8 = pack8<T>(ts);
-#pragma unroll
-                    for (int i = 0; i < D / 32; ++i) {
-                        const int off = (16 * ks + trow) * RW + 32 * i + tcol;
-                        const s16x8 ad = cat4(lds_read_tr16(Ds + off), lds_read_tr16(Ds + off + 8 * RW));
-                        const s16x8 aq = cat4(lds_read_tr16(Qs + off), lds_read_tr16(Qs + off + 8 * RW));
-                        dv[i] = Elem<T>::mfma(ad, bp8, dv[i]);
-                        dk[i] = Elem<T>::mfma(aq, bs8, dk[i]);
-                    }
-                }
+            for (int kk = 0; kk < KR; ++kk) {
+                const s16x8 aq = *reinterpret_cast<const s16x8*>(qrow + 16 * kk + 8 * hi);
+                const s16x8 ad = *reinterpret_cast<const s16x8*>(drow + 16 * kk + 8 * hi);
+                sc = Elem<T>::mfma(aq, __builtin_bit_cast(s16x8, kreg[kk]), sc);
+                dpc = Elem<T>::mfma(ad, __builtin_bit_cast(s16x8, vreg[kk]), dpc);
             }
         }
-        if (it + 1 < total) commit((it + 1) & 1);
     };
 
-    if (total > 0) { issue(0); commit(0); }
-    // one loop body: a second (unmasked) copy of this 256-register body makes the
-    // register allocator shuffle the dK/dV accumulators through AGPRs
-    for (int it = 0; it < total; ++it) step(it, std::integral_constant<bool, CAUSAL>{});
+    // ---- P and dS of tile `it` (buffer s); dS = P (dP - delta), scale applied at the end ----
+    constexpr int NPK = C::F32 ? 1 : BQ / 16;
+    float pd[16], ds[16];
+    s16x8 bp8[NPK], bs8[NPK];
+    auto softmax_ds = [&](int it, int s, const f32x16& sc, const f32x16& dpc, auto mask_tag) FA_INLINE {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const float* lse2 = (const float*)(buf(s) + 2 * C::QTILE * sizeof(T));
+        const float* dels = lse2 + BQ;
+        const int qb0 = tile_q0(it);
+        uint64_t col_ctr = 0;
+        if (DROPOUT)
+            col_ctr = p.offset + (uint64_t)(b * p.H + tile_head(it)) * (uint64_t)p.Sq * (uint64_t)p.Sk + (uint64_t)kj;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse2 + 8 * g + 4 * hi);
+            const f32x4 d4 = *reinterpret_cast<const f32x4*>(dels + 8 * g + 4 * hi);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = 4 * g + e;
+                const int q = qb0 + 8 * g + 4 * hi + e;
+                float pv = fast_exp2(__builtin_fmaf(sc[r], c, -l4[e]));
+                if (MASK && q < kj) pv = 0.f;
+                float dpv = dpc[r];
+                float pdv = pv;
+                if (DROPOUT) {
+                    const float u = philox_uniform(p.seed, col_ctr + (uint64_t)q * (uint64_t)p.Sk);
+                    const float z = u > p.dropout_p ? p.rp : 0.f;
+                    dpv *= z;
+                    pdv *= z;
+                }
+                pd[r] = pdv;
+                ds[r] = pv * (dpv - d4[e]);
+            }
+        }
+        if constexpr (!C::F32) {
+#pragma unroll
+            for (int ks = 0; ks < BQ / 16; ++ks) {
+                bp8[ks] = pack8<T>(pd + 8 * ks);
+                bs8[ks] = pack8<T>(ds + 8 * ks);
+            }
+        }
+    };
+
+    // ---- dV^T += dO^T P,  dK^T += Q^T dS for the tile in buffer s ----
+    auto dkdv_acc = [&](int s) FA_INLINE {
+        const T* Qs = (const T*)buf(s);
+        const T* Ds = Qs + C::QTILE;
+        if constexpr (C::F32) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const int qr = 8 * (t >> 2) + 4 * hi + (t & 3);
+#pragma unroll
+                for (int i = 0; i < D / 32; ++i) {
+                    dv[i] = mfma_f32(Ds[qr * RW + 32 * i + l32], pd[t], dv[i]);
+                    dk[i] = mfma_f32(Qs[qr * RW + 32 * i + l32], ds[t], dk[i]);
+                }
+            }
+        } else {
+            // dO^T / Q^T operands straight from the row-major tiles
+            const int trow = 4 * hi + ((lane & 15) >> 2);
+            const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+#pragma unroll
+            for (int ks = 0; ks < BQ / 16; ++ks)
+#pragma unroll
+                for (int i = 0; i < D / 32; ++i) {
+                    const int off = (16 * ks + trow) * RW + 32 * i + tcol;
+                    const s16x8 ad = cat4(lds_read_tr16(Ds + off), lds_read_tr16(Ds + off + 8 * RW));
+                    const s16x8 aq = cat4(lds_read_tr16(Qs + off), lds_read_tr16(Qs + off + 8 * RW));
+                    dv[i] = Elem<T>::mfma(ad, bp8[ks], dv[i]);
+                    dk[i] = Elem<T>::mfma(aq, bs8[ks], dk[i]);
+                }
+        }
+    };
+
+    // Software pipeline over query tiles.  Iteration `it` issues the MFMAs of
+    // S(it+1), dP(it+1) together with P(it), dS(it) (VALU), then the dK/dV
+    // products of tile `it`.  Three LDS buffers rotate: iteration `it` reads
+    // tiles it (buffer it%3) and it+1, and copies tile it+2 into the buffer
+    // of tile it-1, which every wave finished before the opening barrier.
+    f32x16 sa, da, sb, db;
+    int bcur = 0;  // it % 3
+    auto nxt = [](int s) { return s == 2 ? 0 : s + 1; };
+    if (total > 0) issue(0, 0);
+    if (total > 1) issue(1, 1);
+    sync_tiles();
+    if (total > 0) sdp(0, sa, da);
+
+    auto iter = [&](int it, f32x16& sc, f32x16& dc, f32x16& sn, f32x16& dn, auto mask_tag) FA_INLINE {
+        sync_tiles();
+        const int b1 = nxt(bcur), b2 = nxt(b1);
+        if (it + 2 < total) issue(it + 2, b2);
+        if (it + 1 < total) sdp(b1, sn, dn);
+        softmax_ds(it, bcur, sc, dc, mask_tag);
+        dkdv_acc(bcur);
+        bcur = b1;
+    };
+    // masked tiles first for each query head of the group, then plain ones;
+    // two iterations per trip so the score registers swap roles without copies
+    int it = 0;
+    auto run = [&](int end, auto mask_tag) FA_INLINE {
+        for (; it + 1 < end; it += 2) {
+            iter(it, sa, da, sb, db, mask_tag);
+            iter(it + 1, sb, db, sa, da, mask_tag);
+        }
+        if (it < end) {
+            iter(it, sa, da, sb, db, mask_tag);
+            ++it;
+            sa = sb;
+            da = db;
+        }
+    };
+    for (int g = 0; g < p.group; ++g) {
+        if (CAUSAL) run(g * nq + n_mask, std::true_type{});
+        run((g + 1) * nq, std::false_type{});
+    }
 
     // ---- epilogue: stage dK^T, dV^T through LDS as rows, coalesced stores ----
     constexpr int OW = C::OW;
@@ -268,7 +322,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
     T* Os = (T*)smem + w * 32 * OW;
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
-        lds_barrier();
+        sync_tiles();
         const f32x16* acc = pass == 0 ? dk : dv;
         const float mul = pass == 0 ? p.scale : 1.f;
 #pragma unroll
@@ -331,7 +385,8 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
     __shared__ __attribute__((aligned(16))) T smem[C::SMEM_ELEMS];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6, l32 = lane & 31, hi = lane >> 5;
+    // wave index as a scalar: loop bounds derived from it stay wave-uniform
+    const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
     const int L = xcd_remap(blockIdx.x, gridDim.x);
     const int bh = L / n_qtiles;
     const int qt = n_qtiles - 1 - (L - bh * n_qtiles);
@@ -354,9 +409,9 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
             doreg[i] = ok ? *reinterpret_cast<const uint4*>(drow + d0) : make_uint4(0u, 0u, 0u, 0u);
         }
     }
-    const int64_t si = ((int64_t)b * p.H + h) * p.Sq + qi;
-    const float lse2 = qi < p.Sq ? p.lse[si] * kLog2e : INFINITY;
-    const float del = qi < p.Sq ? p.delta[si] : 0.f;
+    const int64_t wi = ((int64_t)b * p.H + h) * p.sq_pad + qi;  // qi < sq_pad
+    const float lse2 = p.lse2[wi];
+    const float del = p.delta[wi];
     wait_vmem();
     const float c = p.scale_log2;
     uint64_t row_ctr = 0;
@@ -521,7 +576,7 @@ hipError_t launch_bwd_t(const BwdParams& p, int stage, hipStream_t s) {
     if (stage < 0 || stage == 0) {
         constexpr int EPC = 16 / sizeof(T);
         constexpr int RPB = 256 / (D / EPC);
-        const int64_t nrows = (int64_t)p.B * p.Sq * p.H;
+        const int64_t nrows = (int64_t)p.B * p.sq_pad * p.H;
         const int64_t nb = (nrows + RPB - 1) / RPB;
         if (nb > 0) hipLaunchKernelGGL((delta_kernel<T, D>), dim3((unsigned)nb), dim3(256), 0, s, p);
     }

@@ -12,6 +12,11 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Device helpers and kernel-local lambdas are always inlined: an out-of-line
+// call would keep tile descriptors and MFMA accumulators in scratch memory
+// (and turn wave-uniform buffer descriptors into per-lane ones).
+#define FA_INLINE __attribute__((always_inline))
+
 namespace fa {
 
 typedef __bf16 bf16;
@@ -32,34 +37,34 @@ template <typename T> struct Elem;
 template <> struct Elem<bf16> {
     static constexpr bool kF32 = false;
     using Vec8 = bf16x8;
-    __device__ static inline f32x16 mfma(const s16x8& a, const s16x8& b, const f32x16& c) {
+    __device__ FA_INLINE static inline f32x16 mfma(const s16x8& a, const s16x8& b, const f32x16& c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                        __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
     }
-    __device__ static inline short pack1(float x) { return __builtin_bit_cast(short, (bf16)x); }
-    __device__ static inline float unpack1(short x) { return (float)__builtin_bit_cast(bf16, x); }
+    __device__ FA_INLINE static inline short pack1(float x) { return __builtin_bit_cast(short, (bf16)x); }
+    __device__ FA_INLINE static inline float unpack1(short x) { return (float)__builtin_bit_cast(bf16, x); }
 };
 template <> struct Elem<f16> {
     static constexpr bool kF32 = false;
     using Vec8 = f16x8;
-    __device__ static inline f32x16 mfma(const s16x8& a, const s16x8& b, const f32x16& c) {
+    __device__ FA_INLINE static inline f32x16 mfma(const s16x8& a, const s16x8& b, const f32x16& c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                       __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
     }
-    __device__ static inline short pack1(float x) { return __builtin_bit_cast(short, (f16)x); }
-    __device__ static inline float unpack1(short x) { return (float)__builtin_bit_cast(f16, x); }
+    __device__ FA_INLINE static inline short pack1(float x) { return __builtin_bit_cast(short, (f16)x); }
+    __device__ FA_INLINE static inline float unpack1(short x) { return (float)__builtin_bit_cast(f16, x); }
 };
 template <> struct Elem<float> {
     static constexpr bool kF32 = true;
 };
 
-__device__ inline f32x16 mfma_f32(float a, float b, const f32x16& c) {
+__device__ FA_INLINE inline f32x16 mfma_f32(float a, float b, const f32x16& c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
 // 8 x 16-bit elements <-> 8 floats
 template <typename T>
-__device__ inline s16x8 pack8(const float* x) {
+__device__ FA_INLINE inline s16x8 pack8(const float* x) {
     s16x8 r;
 #pragma unroll
     for (int e = 0; e < 8; ++e) r[e] = Elem<T>::pack1(x[e]);
@@ -69,15 +74,15 @@ __device__ inline s16x8 pack8(const float* x) {
 // value held by lane l^32.  (v_permlane32_swap with both operands equal to x
 // would do this in one VALU op, but the compiler folds the per-half select of
 // its two results to the first one, so the LDS-crossbar shuffle is used.)
-__device__ inline float swap_halves(float x) { return __shfl_xor(x, 32, 64); }
+__device__ FA_INLINE inline float swap_halves(float x) { return __shfl_xor(x, 32, 64); }
 
-__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ FA_INLINE inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also fences global
 // memory, which on gfx9 (one counter for vector loads and stores) makes every
 // barrier wait for the in-flight prefetch of the next tile; the kernels never
 // communicate through global memory, so an LDS-scoped fence is sufficient.
-__device__ inline void lds_barrier() {
+__device__ FA_INLINE inline void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
@@ -89,11 +94,11 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 // p must point into __shared__ memory (8-byte aligned); the cast is an
 // address-space cast, not an integer reinterpretation.
-__device__ inline s16x4 lds_read_tr16(const void* p) {
+__device__ FA_INLINE inline s16x4 lds_read_tr16(const void* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
 }
 
-__device__ inline s16x8 cat4(const s16x4& a, const s16x4& b) {
+__device__ FA_INLINE inline s16x8 cat4(const s16x4& a, const s16x4& b) {
     s16x8 r;
     r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
     r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
@@ -104,7 +109,7 @@ __device__ inline s16x8 cat4(const s16x4& a, const s16x4& b) {
 // Philox4x32-10 (Salmon et al., SC'11) with Triton's tl.rand conventions:
 // key = (lo32 seed, hi32 seed), counter = (lo32 c, hi32 c, 0, 0); word 0 is
 // bit-cast to int32, folded x < 0 ? -x - 1 : x, and scaled by 4.6566127342e-10.
-__device__ inline uint32_t philox_word0(uint64_t seed, uint64_t ctr) {
+__device__ FA_INLINE inline uint32_t philox_word0(uint64_t seed, uint64_t ctr) {
     uint32_t c0 = (uint32_t)ctr, c1 = (uint32_t)(ctr >> 32), c2 = 0u, c3 = 0u;
     uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
 #pragma unroll
@@ -121,7 +126,7 @@ __device__ inline uint32_t philox_word0(uint64_t seed, uint64_t ctr) {
     return c0;
 }
 
-__device__ inline float philox_uniform(uint64_t seed, uint64_t ctr) {
+__device__ FA_INLINE inline float philox_uniform(uint64_t seed, uint64_t ctr) {
     int32_t x = (int32_t)philox_word0(seed, ctr);
     x = x < 0 ? -x - 1 : x;
     return __fmul_rn((float)x, 4.6566127342e-10f);
@@ -131,7 +136,7 @@ __device__ inline float philox_uniform(uint64_t seed, uint64_t ctr) {
 // Workgroup-id remap so that consecutive logical tiles land on one XCD.
 // Hardware dispatches workgroup L to XCD L % 8; logical id = (L % 8) * per + L / 8
 // keeps each XCD on a contiguous run of logical tiles (shared K/V stay in one L2).
-__device__ inline int xcd_remap(int L, int N) {
+__device__ FA_INLINE inline int xcd_remap(int L, int N) {
     const int per = N >> 3;
     const int full = per << 3;
     if (L >= full) return L;
@@ -149,7 +154,7 @@ __device__ inline int xcd_remap(int L, int N) {
 // 0 <= nvalid <= rows the byte count fits 32 bits; it is computed without a
 // branch (nvalid <= 0 gives 0) so that a tile load does not end a basic block.
 template <typename T, int D>
-__device__ inline __amdgpu_buffer_rsrc_t row_buffer(const T* base, int64_t row_stride, int nvalid) {
+__device__ FA_INLINE inline __amdgpu_buffer_rsrc_t row_buffer(const T* base, int64_t row_stride, int nvalid) {
     const int nv = max(nvalid, 0);
     const int bytes = ((nv - 1) * (int)row_stride + D) * (int)sizeof(T) * min(nv, 1);
     // dword 3: DATA_FORMAT = 32 (untyped dword access), no swizzle, no stride
@@ -160,9 +165,9 @@ __device__ inline __amdgpu_buffer_rsrc_t row_buffer(const T* base, int64_t row_s
 // per-lane register operands (Q, dO, K, V rows, LSE, delta) are loaded, so the
 // compiler's wait tracking starts every tile loop with nothing pending and does
 // not re-wait for them (together with the next tile's prefetch) each iteration.
-__device__ inline void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+__device__ FA_INLINE inline void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
-__device__ inline uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, int byte_offset) {
+__device__ FA_INLINE inline uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, int byte_offset) {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 0));
 }
 
@@ -173,7 +178,7 @@ __device__ inline uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, int byte_offset)
 // rows 16s + {4h .. 4h+3, 8+4h .. 8+4h+3} (h = l/32).  Storing row r at column
 // slot(r) = r with bits 2 and 3 swapped makes those 8 rows contiguous
 // (slots 16s + 8h .. 16s + 8h + 7), so one ds_read_b128 fetches the operand.
-__device__ inline int slot_of_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+__device__ FA_INLINE inline int slot_of_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
 // Global -> register -> LDS staging of a [R][D] tile of 16-bit elements.
 // Each thread owns units of 4 rows x 8 columns (four 16-byte loads) and can
@@ -200,12 +205,12 @@ struct Tile16 {
     static constexpr int PER = (UNITS + NT - 1) / NT;
     uint4 r[PER][4];
 
-    __device__ static inline int row_group(int u) { return ROWS_FAST ? u % RG : 4 * ((u >> 2) / CG) + (u & 3); }
-    __device__ static inline int col_group(int u) { return ROWS_FAST ? u / RG : (u >> 2) % CG; }
+    __device__ FA_INLINE static inline int row_group(int u) { return ROWS_FAST ? u % RG : 4 * ((u >> 2) / CG) + (u & 3); }
+    __device__ FA_INLINE static inline int col_group(int u) { return ROWS_FAST ? u / RG : (u >> 2) % CG; }
 
     // Rows >= nvalid read as zeros (buffer range check); no branches or
     // selects on the loaded data, so nothing forces an early wait on the loads.
-    __device__ inline void load(const T* __restrict__ base, int64_t row_stride, int nvalid, int tid) {
+    __device__ FA_INLINE inline void load(const T* __restrict__ base, int64_t row_stride, int nvalid, int tid) {
         const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D>(base, row_stride, nvalid);
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
@@ -219,7 +224,7 @@ struct Tile16 {
         }
     }
     template <int W>
-    __device__ inline void store_rows(T* lds, int tid) const {
+    __device__ FA_INLINE inline void store_rows(T* lds, int tid) const {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int u = tid + i * NT;
@@ -231,7 +236,7 @@ struct Tile16 {
         }
     }
     template <int W>
-    __device__ inline void store_trans(T* ldsT, int tid) const {
+    __device__ FA_INLINE inline void store_trans(T* ldsT, int tid) const {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int u = tid + i * NT;
@@ -261,7 +266,7 @@ struct Tile16 {
 // builtin made the host pass emit launch stubs only for the first
 // instantiation of each kernel (the library then fails to load).
 template <typename T>
-__device__ inline void dma_load16(__amdgpu_buffer_rsrc_t rs, T* lds, int byte_offset) {
+__device__ FA_INLINE inline void dma_load16(__amdgpu_buffer_rsrc_t rs, T* lds, int byte_offset) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, byte_offset, 0, 0, 0);
 }
 
@@ -290,7 +295,7 @@ struct DmaTile {
 
     // wave_id must be wave-uniform (readfirstlane): it selects the LDS
     // destination, which the hardware takes from a scalar register (M0).
-    __device__ inline void init(int64_t row_stride, int lane, int wave_id) {
+    __device__ FA_INLINE inline void init(int64_t row_stride, int lane, int wave_id) {
         wave = wave_id;
 #pragma unroll
         for (int t = 0; t < PER; ++t) {
@@ -299,7 +304,7 @@ struct DmaTile {
             off[t] = (row * (int)row_stride + col * EPC) * (int)sizeof(T);
         }
     }
-    __device__ inline void load(const T* base, int64_t row_stride, int nvalid, T* lds, int lane) const {
+    __device__ FA_INLINE inline void load(const T* base, int64_t row_stride, int nvalid, T* lds, int lane) const {
         const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D>(base, row_stride, nvalid);
 #pragma unroll
         for (int t = 0; t < PER; ++t) {
@@ -323,7 +328,7 @@ struct TileStage {
     static constexpr int PER = (TOTAL + NT - 1) / NT;
     uint4 r[PER];
 
-    __device__ inline void load(const T* __restrict__ base, int64_t row_stride, int nvalid, int tid) {
+    __device__ FA_INLINE inline void load(const T* __restrict__ base, int64_t row_stride, int nvalid, int tid) {
         const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D>(base, row_stride, nvalid);
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
@@ -334,7 +339,7 @@ struct TileStage {
         }
     }
     template <int LDSW>
-    __device__ inline void store(T* lds, int tid) const {
+    __device__ FA_INLINE inline void store(T* lds, int tid) const {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int c = tid + i * NT;

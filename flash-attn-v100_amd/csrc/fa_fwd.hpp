@@ -52,7 +52,8 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     __shared__ __attribute__((aligned(16))) T smem[C::SMEM_ELEMS];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6, l32 = lane & 31, hi = lane >> 5;
+    // wave index as a scalar: loop bounds derived from it stay wave-uniform
+    const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
 
     const int L = xcd_remap(blockIdx.x, gridDim.x);
     const int bh = L / p.n_qtiles;

@@ -38,7 +38,8 @@ struct BwdParams {
     void* dq;
     void* dk;
     void* dv;
-    float* delta;  // workspace (B, H, Sq)
+    float* delta;  // workspace: rowsum(dO * O), rows of sq_pad per (batch, head)
+    float* lse2;   // workspace: LSE * log2(e), same layout; +inf past Sq
     int64_t q_sb, q_ss, q_sh;
     int64_t k_sb, k_ss, k_sh;
     int64_t v_sb, v_ss, v_sh;
@@ -48,9 +49,14 @@ struct BwdParams {
     int64_t dk_sb, dk_ss, dk_sh;
     int64_t dv_sb, dv_ss, dv_sh;
     int B, Sq, Sk, H, Hkv, group;
+    int sq_pad;  // Sq rounded up to kSqPad
     float scale, scale_log2, dropout_p, rp;
     uint64_t seed, offset;
 };
+
+// per-(batch, head) rows of the backward workspace are padded to a multiple
+// of this many queries, so query tiles read whole rows without range checks
+constexpr int kSqPad = 128;
 
 // dtype-specific launchers (fa_kernels_{bf16,f16,f32}.hip)
 hipError_t launch_fwd_bf16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
