@@ -62,11 +62,11 @@ int32_t check_span(const int64_t st[4], int32_t S, int32_t D, int es) {
     return span < (1LL << 31) ? FA_OK : FA_ERR_TOO_LARGE;
 }
 
-// One of the two float32 workspace arrays (delta, LSE * log2 e): B * H rows of
-// Sq rounded up to kSqPad, rounded up to 256 bytes.
-size_t ws_part_bytes(const fa_bwd_args* a) {
+// Backward workspace: B * H rows of 2 * sq_pad float32 (LSE * log2 e, then
+// delta), sq_pad = Sq rounded up to kSqPad; total rounded up to 256 bytes.
+size_t ws_bytes_for(const fa_bwd_args* a) {
     const size_t sq_pad = ((size_t)a->seqlen_q + fa::kSqPad - 1) / fa::kSqPad * fa::kSqPad;
-    const size_t n = (size_t)a->batch * (size_t)a->num_heads * sq_pad * sizeof(float);
+    const size_t n = (size_t)a->batch * (size_t)a->num_heads * 2 * sq_pad * sizeof(float);
     return (n + 255) & ~(size_t)255;
 }
 
@@ -160,7 +160,7 @@ size_t fa_bwd_workspace_size(const fa_bwd_args* a) {
     if (check_common(a->batch, a->seqlen_q, a->seqlen_k, a->num_heads, a->num_heads_kv, a->head_dim, a->dtype,
                      a->scale, a->dropout_p))
         return 0;
-    return 2 * ws_part_bytes(a);
+    return ws_bytes_for(a);
 }
 
 int32_t fa_bwd_check(const fa_bwd_args* a, size_t ws_bytes) {
@@ -210,9 +210,10 @@ int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int
     p.dq = a->dq;
     p.dk = a->dk;
     p.dv = a->dv;
-    p.delta = (float*)workspace;
-    p.lse2 = (float*)((char*)workspace + ws_part_bytes(a));
     p.sq_pad = (a->seqlen_q + fa::kSqPad - 1) / fa::kSqPad * fa::kSqPad;
+    p.ws_stride = 2 * p.sq_pad;
+    p.lse2 = (float*)workspace;
+    p.delta = (float*)workspace + p.sq_pad;
     split(a->q_stride, p.q_sb, p.q_ss, p.q_sh);
     split(a->k_stride, p.k_sb, p.k_ss, p.k_sh);
     split(a->v_stride, p.v_sb, p.v_ss, p.v_sh);

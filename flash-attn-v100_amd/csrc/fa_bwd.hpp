@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void delta_kernel(const BwdParams p) {
 #pragma unroll
     for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
     if (row < nrows && part == 0) {
-        const int64_t wi = ((int64_t)b * p.H + h) * p.sq_pad + i;
+        const int64_t wi = ((int64_t)b * p.H + h) * p.ws_stride + i;
         p.delta[wi] = acc;
         p.lse2[wi] = i < p.Sq ? p.lse[((int64_t)b * p.H + h) * p.Sq + i] * kLog2e : INFINITY;
     }
@@ -84,8 +84,11 @@ struct DkdvCfg {
     // in the 256-byte bank window
     static constexpr int RW = D + (F32 ? 4 : (D == 64 ? 8 : 24));
     static constexpr int QTILE = BQ * RW;
+    // Q (waves 0-1) and dO (waves 2-3) tiles are copied global -> LDS directly
+    using Rows = DmaRows<T, BQ, D, RW, NW / 2>;
+    static constexpr int QALLOC = Rows::LDS_BYTES;  // tile + copy slack
     // per buffer: Q rows, dO rows, then LSE * log2 e [BQ] and delta [BQ] as floats
-    static constexpr int BUF_BYTES = 2 * QTILE * (int)sizeof(T) + 2 * BQ * 4;
+    static constexpr int BUF_BYTES = 2 * QALLOC + 2 * BQ * 4;
     static constexpr int NBUF = 3;                  // tiles t, t+1 read while t+2 lands
     static constexpr int OW = D + (F32 ? 4 : 8);    // output staging stride
     static constexpr int SMEM_BYTES_RAW = NBUF * BUF_BYTES;
@@ -95,7 +98,7 @@ struct DkdvCfg {
 };
 
 template <typename T, int D, bool CAUSAL, bool DROPOUT>
-__global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const int n_ktiles) {
+__global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const int n_ktiles) {
     using C = DkdvCfg<T, D>;
     constexpr int BQ = C::BQ, RW = C::RW;
     __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
@@ -141,25 +144,39 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
     const int n_mask = CAUSAL ? min(nq, max(0, (kw0 + 31 + BQ - 1) / BQ - qt_begin)) : 0;
 
     // ---- tiles: Q, dO rows and the LSE / delta rows, global -> LDS directly ----
-    const int wv = __builtin_amdgcn_readfirstlane(w);
-    DmaTile<T, BQ, D, RW, C::NW> qdma, ddma;
-    DmaTile<float, 1, BQ, BQ, C::NW> ldma;
-    qdma.init(p.q_ss, lane, wv);
-    ddma.init(p.do_ss, lane, wv);
-    ldma.init(BQ, lane, wv);
+    // waves 0-1 copy Q, waves 2-3 copy dO (scalar selects, no branches); every
+    // wave copies the tile's LSE * log2 e and delta (one dword per lane, the
+    // same values), so a tile copy is branch-free and can sit between MFMAs
+    const bool copy_q = w < C::NW / 2;
+    typename C::Rows rows;
+    rows.init(copy_q ? p.q_ss : p.do_ss, lane, w % (C::NW / 2));
+    const int ws_lane = 4 * (lane < BQ ? lane : p.sq_pad + lane - BQ);
+    static_assert(2 * BQ == 64, "one dword per lane for LSE and delta");
     auto buf = [&](int s) -> char* { return smem + s * C::BUF_BYTES; };
     auto tile_head = [&](int it) { return hk * p.group + it / nq; };
     auto tile_q0 = [&](int it) { return (qt_begin + it % nq) * BQ; };
-    auto issue = [&](int it, int s) FA_INLINE {
+    // copy of tile `it` into buffer s, in three parts (PART 2 also copies the
+    // LSE / delta row) so that they can be spread between MFMAs
+    constexpr int P3 = (C::Rows::PER + 2) / 3;
+    auto issue = [&](int it, int s, auto part_tag) FA_INLINE {
+        constexpr int PART = decltype(part_tag)::value;
         const int hh = tile_head(it), qb0 = tile_q0(it);
         char* bp = buf(s);
-        qdma.load((const T*)p.q + b * p.q_sb + (int64_t)qb0 * p.q_ss + hh * p.q_sh, p.q_ss, p.Sq - qb0, (T*)bp, lane);
-        ddma.load((const T*)p.dout + b * p.do_sb + (int64_t)qb0 * p.do_ss + hh * p.do_sh, p.do_ss, p.Sq - qb0,
-                  (T*)bp + C::QTILE, lane);
-        const int64_t wrow = ((int64_t)b * p.H + hh) * p.sq_pad + qb0;  // qb0 + BQ <= sq_pad
-        float* f = (float*)(bp + 2 * C::QTILE * sizeof(T));
-        ldma.load(p.lse2 + wrow, BQ, 1, f, lane);
-        ldma.load(p.delta + wrow, BQ, 1, f + BQ, lane);
+        const T* src = copy_q ? (const T*)p.q + b * p.q_sb + (int64_t)qb0 * p.q_ss + hh * p.q_sh
+                              : (const T*)p.dout + b * p.do_sb + (int64_t)qb0 * p.do_ss + hh * p.do_sh;
+        rows.template load<PART * P3, (PART + 1) * P3>(src, copy_q ? p.q_ss : p.do_ss, p.Sq - qb0,
+                                                        (T*)(bp + (copy_q ? 0 : C::QALLOC)));
+        if constexpr (PART == 2) {
+            const float* wrow = p.lse2 + ((int64_t)b * p.H + hh) * p.ws_stride + qb0;  // qb0 + BQ <= sq_pad
+            const __amdgpu_buffer_rsrc_t rs =
+                __builtin_amdgcn_make_buffer_rsrc((void*)wrow, (short)0, (p.ws_stride - qb0) * 4, 0x00020000);
+            dma_load4(rs, bp + 2 * C::QALLOC, ws_lane);
+        }
+    };
+    auto issue_all = [&](int it, int s) FA_INLINE {
+        issue(it, s, std::integral_constant<int, 0>{});
+        issue(it, s, std::integral_constant<int, 1>{});
+        issue(it, s, std::integral_constant<int, 2>{});
     };
     // direct-to-LDS copies complete when the issuing wave's vmcnt drains
     auto sync_tiles = [&]() {
@@ -168,16 +185,19 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
     };
 
     // ---- S = Q K^T and dP = dO V^T for the tile in buffer s (C[q][key]) ----
-    auto sdp = [&](int s, f32x16& sc, f32x16& dpc) FA_INLINE {
+    auto sdp = [&](int s, f32x16& sc, f32x16& dpc, auto lo_tag, auto hi_tag) FA_INLINE {
+        constexpr int LO = decltype(lo_tag)::value, HI = decltype(hi_tag)::value;
         const T* Qs = (const T*)buf(s);
-        const T* Ds = Qs + C::QTILE;
-        sc = f32x16{};
-        dpc = f32x16{};
+        const T* Ds = (const T*)(buf(s) + C::QALLOC);
+        if constexpr (LO == 0) {
+            sc = f32x16{};
+            dpc = f32x16{};
+        }
         const T* qrow = Qs + l32 * RW;
         const T* drow = Ds + l32 * RW;
         if constexpr (C::F32) {
 #pragma unroll
-            for (int i = 0; i < KR; ++i) {
+            for (int i = LO; i < HI; ++i) {
                 const f32x4 aq = *reinterpret_cast<const f32x4*>(qrow + hi * (D / 2) + 4 * i);
                 const f32x4 ad = *reinterpret_cast<const f32x4*>(drow + hi * (D / 2) + 4 * i);
                 const f32x4 bk = __builtin_bit_cast(f32x4, kreg[i]);
@@ -190,7 +210,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
             }
         } else {
 #pragma unroll
-            for (int kk = 0; kk < KR; ++kk) {
+            for (int kk = LO; kk < HI; ++kk) {
                 const s16x8 aq = *reinterpret_cast<const s16x8*>(qrow + 16 * kk + 8 * hi);
                 const s16x8 ad = *reinterpret_cast<const s16x8*>(drow + 16 * kk + 8 * hi);
                 sc = Elem<T>::mfma(aq, __builtin_bit_cast(s16x8, kreg[kk]), sc);
@@ -205,7 +225,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
     s16x8 bp8[NPK], bs8[NPK];
     auto softmax_ds = [&](int it, int s, const f32x16& sc, const f32x16& dpc, auto mask_tag) FA_INLINE {
         constexpr bool MASK = decltype(mask_tag)::value;
-        const float* lse2 = (const float*)(buf(s) + 2 * C::QTILE * sizeof(T));
+        const float* lse2 = (const float*)(buf(s) + 2 * C::QALLOC);
         const float* dels = lse2 + BQ;
         const int qb0 = tile_q0(it);
         uint64_t col_ctr = 0;
@@ -243,12 +263,14 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
     };
 
     // ---- dV^T += dO^T P,  dK^T += Q^T dS for the tile in buffer s ----
-    auto dkdv_acc = [&](int s) FA_INLINE {
+    // half H (0 or 1) of the products: query rows [16 H, 16 H + 16)
+    auto dkdv_acc = [&](int s, auto half_tag) FA_INLINE {
+        constexpr int H2 = decltype(half_tag)::value;
         const T* Qs = (const T*)buf(s);
-        const T* Ds = Qs + C::QTILE;
+        const T* Ds = (const T*)(buf(s) + C::QALLOC);
         if constexpr (C::F32) {
 #pragma unroll
-            for (int t = 0; t < 16; ++t) {
+            for (int t = 8 * H2; t < 8 * H2 + 8; ++t) {
                 const int qr = 8 * (t >> 2) + 4 * hi + (t & 3);
 #pragma unroll
                 for (int i = 0; i < D / 32; ++i) {
@@ -260,8 +282,8 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
             // dO^T / Q^T operands straight from the row-major tiles
             const int trow = 4 * hi + ((lane & 15) >> 2);
             const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-#pragma unroll
-            for (int ks = 0; ks < BQ / 16; ++ks)
+            static_assert(BQ == 32, "two 16-query halves");
+            constexpr int ks = H2;
 #pragma unroll
                 for (int i = 0; i < D / 32; ++i) {
                     const int off = (16 * ks + trow) * RW + 32 * i + tcol;
@@ -273,46 +295,38 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const i
         }
     };
 
-    // Software pipeline over query tiles.  Iteration `it` issues the MFMAs of
-    // S(it+1), dP(it+1) together with P(it), dS(it) (VALU), then the dK/dV
-    // products of tile `it`.  Three LDS buffers rotate: iteration `it` reads
-    // tiles it (buffer it%3) and it+1, and copies tile it+2 into the buffer
-    // of tile it-1, which every wave finished before the opening barrier.
-    f32x16 sa, da, sb, db;
+    // Loop over query tiles.  Three LDS buffers rotate: iteration `it` reads
+    // tile it (buffer it%3) while the copies of tiles it+1 and it+2 are in
+    // flight; tile it+2 goes into the buffer of tile it-1, which every wave
+    // finished before the opening barrier.  Past the last tile the copies
+    // repeat it, which keeps the loop body free of branches.  Two workgroups
+    // share a CU (255 registers per lane), so each SIMD interleaves the
+    // MFMA, softmax and LDS phases of two waves.
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using IK = std::integral_constant<int, KR>;
+    if (total > 0) {
+        issue_all(0, 0);
+        issue_all(min(1, total - 1), 1);
+    }
+    f32x16 sc, dpc;
     int bcur = 0;  // it % 3
     auto nxt = [](int s) { return s == 2 ? 0 : s + 1; };
-    if (total > 0) issue(0, 0);
-    if (total > 1) issue(1, 1);
-    sync_tiles();
-    if (total > 0) sdp(0, sa, da);
-
-    auto iter = [&](int it, f32x16& sc, f32x16& dc, f32x16& sn, f32x16& dn, auto mask_tag) FA_INLINE {
+    auto iter = [&](int it, auto mask_tag) FA_INLINE {
         sync_tiles();
-        const int b1 = nxt(bcur), b2 = nxt(b1);
-        if (it + 2 < total) issue(it + 2, b2);
-        if (it + 1 < total) sdp(b1, sn, dn);
-        softmax_ds(it, bcur, sc, dc, mask_tag);
-        dkdv_acc(bcur);
-        bcur = b1;
+        issue_all(min(it + 2, total - 1), nxt(nxt(bcur)));
+        sdp(bcur, sc, dpc, I0{}, IK{});
+        softmax_ds(it, bcur, sc, dpc, mask_tag);
+        dkdv_acc(bcur, I0{});
+        dkdv_acc(bcur, I1{});
+        bcur = nxt(bcur);
     };
-    // masked tiles first for each query head of the group, then plain ones;
-    // two iterations per trip so the score registers swap roles without copies
+    // masked tiles first for each query head of the group, then plain ones
     int it = 0;
-    auto run = [&](int end, auto mask_tag) FA_INLINE {
-        for (; it + 1 < end; it += 2) {
-            iter(it, sa, da, sb, db, mask_tag);
-            iter(it + 1, sb, db, sa, da, mask_tag);
-        }
-        if (it < end) {
-            iter(it, sa, da, sb, db, mask_tag);
-            ++it;
-            sa = sb;
-            da = db;
-        }
-    };
     for (int g = 0; g < p.group; ++g) {
-        if (CAUSAL) run(g * nq + n_mask, std::true_type{});
-        run((g + 1) * nq, std::false_type{});
+        if (CAUSAL)
+            for (; it < g * nq + n_mask; ++it) iter(it, std::true_type{});
+        for (; it < (g + 1) * nq; ++it) iter(it, std::false_type{});
     }
 
     // ---- epilogue: stage dK^T, dV^T through LDS as rows, coalesced stores ----
@@ -409,7 +423,7 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
             doreg[i] = ok ? *reinterpret_cast<const uint4*>(drow + d0) : make_uint4(0u, 0u, 0u, 0u);
         }
     }
-    const int64_t wi = ((int64_t)b * p.H + h) * p.sq_pad + qi;  // qi < sq_pad
+    const int64_t wi = ((int64_t)b * p.H + h) * p.ws_stride + qi;  // qi < sq_pad
     const float lse2 = p.lse2[wi];
     const float del = p.delta[wi];
     wait_vmem();

@@ -317,6 +317,49 @@ struct DmaTile {
     }
 };
 
+// Branch-free variant for software-pipelined loops: the tile is copied by
+// NWAVES waves with the same number of whole instructions each; the spare
+// lanes of the last instructions copy rows past R into slack space that the
+// caller allocates (LDS_BYTES per tile).  No per-lane or per-wave branch, so
+// the copies can be scheduled between MFMAs.
+template <typename T, int R, int D, int W, int NWAVES>
+struct DmaRows {
+    static constexpr int EPC = 16 / (int)sizeof(T);
+    static constexpr int CD = D / EPC;
+    static constexpr int CW = W / EPC;
+    static_assert(D % EPC == 0 && W % EPC == 0 && W >= D, "16-byte chunked rows");
+    static constexpr int NI = ((R * CW + 63) / 64 + NWAVES - 1) / NWAVES * NWAVES;
+    static constexpr int PER = NI / NWAVES;
+    static constexpr int LDS_BYTES = NI * 64 * 16;
+    int off[PER];
+    int wave;
+
+    // wave_id: this wave's index among the NWAVES copying waves (wave-uniform)
+    __device__ FA_INLINE inline void init(int64_t row_stride, int lane, int wave_id) {
+        wave = wave_id;
+#pragma unroll
+        for (int t = 0; t < PER; ++t) {
+            const int c = 64 * (wave + NWAVES * t) + lane;
+            const int row = c / CW, col = min(c % CW, CD - 1);
+            off[t] = (row * (int)row_stride + col * EPC) * (int)sizeof(T);
+        }
+    }
+    // copies this wave's instructions [T0, T1) of the tile
+    template <int T0 = 0, int T1 = PER>
+    __device__ FA_INLINE inline void load(const T* base, int64_t row_stride, int nvalid, T* lds) const {
+        const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D>(base, row_stride, nvalid);
+#pragma unroll
+        for (int t = T0; t < (T1 < PER ? T1 : PER); ++t) dma_load16(rs, lds + 64 * (wave + NWAVES * t) * EPC, off[t]);
+    }
+};
+
+// One dword per lane global -> LDS (buffer_load_dword ... lds): lane l writes
+// LDS bytes [4 l, 4 l + 4) past `lds` (wave-uniform).
+template <typename T>
+__device__ FA_INLINE inline void dma_load4(__amdgpu_buffer_rsrc_t rs, T* lds, int byte_offset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 4, byte_offset, 0, 0, 0);
+}
+
 // ---------------------------------------------------------------------------
 // Global -> register -> LDS staging of a [ROWS][D] tile of T with 16-byte
 // chunks (LDS row stride LDSW elements); same tail handling as Tile16.

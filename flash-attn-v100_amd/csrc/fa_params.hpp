@@ -38,8 +38,10 @@ struct BwdParams {
     void* dq;
     void* dk;
     void* dv;
-    float* delta;  // workspace: rowsum(dO * O), rows of sq_pad per (batch, head)
-    float* lse2;   // workspace: LSE * log2(e), same layout; +inf past Sq
+    // workspace: per (batch, head) a row of ws_stride = 2 * sq_pad floats,
+    // LSE * log2(e) (+inf past Sq) then rowsum(dO * O) (0 past Sq)
+    float* lse2;   // = workspace
+    float* delta;  // = workspace + sq_pad
     int64_t q_sb, q_ss, q_sh;
     int64_t k_sb, k_ss, k_sh;
     int64_t v_sb, v_ss, v_sh;
@@ -49,7 +51,8 @@ struct BwdParams {
     int64_t dk_sb, dk_ss, dk_sh;
     int64_t dv_sb, dv_ss, dv_sh;
     int B, Sq, Sk, H, Hkv, group;
-    int sq_pad;  // Sq rounded up to kSqPad
+    int sq_pad;     // Sq rounded up to kSqPad
+    int ws_stride;  // 2 * sq_pad
     float scale, scale_log2, dropout_p, rp;
     uint64_t seed, offset;
 };

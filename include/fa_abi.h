@@ -136,10 +136,10 @@ int32_t fa_fwd_check(const fa_fwd_args* args);
  * kernels/forward_kernel.py:246-387 (launch at :349-385). */
 int32_t fa_fwd(const fa_fwd_args* args, void* hip_stream);
 
-/* Bytes of device workspace fa_bwd needs: two float32 arrays of B * H rows
- * of Sq rounded up to 128 (delta = rowsum(dO * O) and LSE * log2 e, written by
- * the pre-pass), each rounded up to 256 bytes; 0 on invalid arguments.  The
- * reference had no workspace (it recomputed delta per tile pair,
+/* Bytes of device workspace fa_bwd needs: B * H rows of 2 * sq_pad float32
+ * (sq_pad = Sq rounded up to 128; LSE * log2 e then delta = rowsum(dO * O),
+ * written by the pre-pass), rounded up to 256 bytes; 0 on invalid arguments.
+ * The reference had no workspace (it recomputed delta per tile pair,
  * backward_kernel.py:119-121). */
 size_t fa_bwd_workspace_size(const fa_bwd_args* args);
 

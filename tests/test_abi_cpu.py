@@ -175,7 +175,7 @@ def test_bwd_workspace_and_checks():
     a = _lib.bwd_args(q, q, q, q, q, lse, q, q, q, True, 0.125, 0.0, 0, 0)
     ws = lib.fa_bwd_workspace_size(ctypes.byref(a))
     sq_pad = (S + 127) // 128 * 128
-    assert ws == 2 * (((B * H * sq_pad * 4 + 255) // 256) * 256)
+    assert ws == ((B * H * 2 * sq_pad * 4 + 255) // 256) * 256
     assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_OK"]
     assert lib.fa_bwd_check(ctypes.byref(a), ws - 4) == CODES["FA_ERR_WORKSPACE"]
     assert lib.fa_bwd_stage(ctypes.byref(a), None, ws, 3, None) == CODES["FA_ERR_SHAPE"]
