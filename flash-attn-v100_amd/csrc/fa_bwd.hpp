@@ -379,15 +379,17 @@ struct DqCfg {
     static constexpr int NT = 64 * NW;
     static constexpr int BM = 32 * NW;            // queries per workgroup
     static constexpr int BN = 32;                 // keys per tile
-    static constexpr int KW = D + (F32 ? 4 : 8);  // K / V row stride (elements)
-    static constexpr int TW = BN + 8;             // K^T row stride (16-bit types)
-    static constexpr int KTILE = BN * KW;
-    static constexpr int KTTILE = F32 ? 0 : D * TW;
-    static constexpr int BUF = 2 * KTILE + KTTILE;  // K rows, V rows, K^T
+    // K / V row stride: conflict-free ds_read_b128 row reads and (16-bit)
+    // ds_read_b64_tr_b16 reads of K^T, as for the dK/dV tiles
+    static constexpr int KW = D + (F32 ? 4 : (D == 64 ? 8 : 24));
+    // K (waves 0-1) and V (waves 2-3) tiles are copied global -> LDS directly
+    using Rows = DmaRows<T, BN, D, KW, NW / 2>;
+    static constexpr int KALLOC = Rows::LDS_BYTES;  // tile + copy slack
+    static constexpr int BUF_BYTES = 2 * KALLOC;    // K rows, V rows
+    static constexpr int NBUF = 3;
     static constexpr int OW = D + (F32 ? 4 : 8);
-    static constexpr int SMEM_ELEMS_RAW = 2 * BUF;
-    static constexpr int STAGE_ELEMS = NW * 32 * OW;
-    static constexpr int SMEM_ELEMS = SMEM_ELEMS_RAW > STAGE_ELEMS ? SMEM_ELEMS_RAW : STAGE_ELEMS;
+    static constexpr int STAGE_BYTES = NW * 32 * OW * (int)sizeof(T);
+    static constexpr int SMEM_BYTES = NBUF * BUF_BYTES > STAGE_BYTES ? NBUF * BUF_BYTES : STAGE_BYTES;
     // fp32 at D=128 needs more than 256 registers per lane (Q, dO and dQ^T in fp32)
     static constexpr int MIN_BLOCKS = (F32 && D == 128) ? 1 : 2;
 };
@@ -395,8 +397,8 @@ struct DqCfg {
 template <typename T, int D, bool CAUSAL, bool DROPOUT>
 __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(const BwdParams p, const int n_qtiles) {
     using C = DqCfg<T, D>;
-    constexpr int BN = C::BN, KW = C::KW, TW = C::TW;
-    __shared__ __attribute__((aligned(16))) T smem[C::SMEM_ELEMS];
+    constexpr int BN = C::BN, KW = C::KW;
+    __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
 
     const int tid = threadIdx.x;
     // wave index as a scalar: loop bounds derived from it stay wave-uniform
@@ -441,44 +443,45 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
     int n_plain = min(n_tiles, p.Sk / BN);
     if (CAUSAL) n_plain = min(n_plain, (q0 + 1) / BN);
 
+    // ---- K / V tiles: waves 0-1 copy K, waves 2-3 copy V, global -> LDS ----
     const T* kbase = (const T*)p.k + b * p.k_sb + hk * p.k_sh;
     const T* vbase = (const T*)p.v + b * p.v_sb + hk * p.v_sh;
-    // 16-bit types: waves 0-1 stage the K tile (rows and K^T), waves 2-3 the
-    // V tile; fp32 stages both with all threads.
-    using KStage = typename std::conditional<C::F32, TileStage<T, BN, D, C::NT>, Tile16<T, BN, D, C::NT / 2>>::type;
-    KStage kst, vst;
-    const bool stage_k = tid < C::NT / 2;  // wave-uniform
-    const int stid = tid & (C::NT / 2 - 1);
-    auto load_tile = [&](int k0) {
-        if constexpr (C::F32) {
-            kst.load(kbase + (int64_t)k0 * p.k_ss, p.k_ss, p.Sk - k0, tid);
-            vst.load(vbase + (int64_t)k0 * p.v_ss, p.v_ss, p.Sk - k0, tid);
-        } else {
-            if (stage_k) kst.load(kbase + (int64_t)k0 * p.k_ss, p.k_ss, p.Sk - k0, stid);
-            else kst.load(vbase + (int64_t)k0 * p.v_ss, p.v_ss, p.Sk - k0, stid);
-        }
+    const bool copy_k = w < C::NW / 2;
+    typename C::Rows rows;
+    rows.init(copy_k ? p.k_ss : p.v_ss, lane, w % (C::NW / 2));
+    auto buf = [&](int s) -> char* { return smem + s * C::BUF_BYTES; };
+    auto issue = [&](int j, int s) FA_INLINE {
+        const int k0 = j * BN;
+        const T* src = copy_k ? kbase + (int64_t)k0 * p.k_ss : vbase + (int64_t)k0 * p.v_ss;
+        rows.load(src, copy_k ? p.k_ss : p.v_ss, p.Sk - k0, (T*)(buf(s) + (copy_k ? 0 : C::KALLOC)));
     };
-    auto store_tile = [&](int buf) {
-        T* base = smem + buf * C::BUF;
-        if constexpr (C::F32) {
-            kst.template store<KW>(base, tid);
-            vst.template store<KW>(base + C::KTILE, tid);
-        } else {
-            kst.template store_rows<KW>(base + (stage_k ? 0 : C::KTILE), stid);
-            if (stage_k) kst.template store_trans<TW>(base + 2 * C::KTILE, stid);
-        }
+    // direct-to-LDS copies complete when the issuing wave's vmcnt drains
+    auto sync_tiles = [&]() {
+        wait_vmem();
+        lds_barrier();
     };
 
-    auto step = [&](int j, auto mask_tag) {
+    // Three LDS buffers rotate: tile j is read from buffer j%3 while tiles
+    // j+1 and j+2 are in flight; tile j+2 goes into the buffer of tile j-1,
+    // which every wave finished before the opening barrier.  Past the last
+    // tile the copies repeat it (never read), so the copy is branch-free.
+    int bcur = 0;
+    auto nxt = [](int s) { return s == 2 ? 0 : s + 1; };
+    if (n_tiles > 0) {
+        issue(0, 0);
+        issue(min(1, n_tiles - 1), 1);
+    }
+
+    auto step = [&](int j, auto mask_tag) FA_INLINE {
         constexpr bool MASK = decltype(mask_tag)::value;
         const int k0 = j * BN;
-        if (j + 1 < n_tiles) load_tile(k0 + BN);
-        lds_barrier();
-        const T* Ks = smem + (j & 1) * C::BUF;
-        const T* Vs = Ks + C::KTILE;
-        const T* KT = Ks + 2 * C::KTILE;
+        sync_tiles();
+        issue(min(j + 2, n_tiles - 1), nxt(nxt(bcur)));
+        const T* Ks = (const T*)buf(bcur);
+        const T* Vs = (const T*)(buf(bcur) + C::KALLOC);
         const bool active = !MASK || !CAUSAL || k0 <= qw0 + 31;
         if (active) {
+            // ---- S^T = K Q^T, dP^T = V dO^T (C[key][query]) ----
             f32x16 s = f32x16{}, dp = f32x16{};
             const T* krow = Ks + l32 * KW;
             const T* vrow = Vs + l32 * KW;
@@ -504,6 +507,7 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
                     dp = Elem<T>::mfma(av, __builtin_bit_cast(s16x8, doreg[kk]), dp);
                 }
             }
+            // ---- dS^T = P^T (dP^T - delta); scale applied at the end ----
             const bool need_mask = MASK && ((k0 + BN > p.Sk) || (CAUSAL && k0 + BN - 1 > qw0));
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -515,8 +519,9 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
                     const float u = philox_uniform(p.seed, row_ctr + (uint64_t)key);
                     dpv *= u > p.dropout_p ? p.rp : 0.f;
                 }
-                s[r] = pv * (dpv - del);  // dS
+                s[r] = pv * (dpv - del);
             }
+            // ---- dQ^T += K^T dS^T ----
             if constexpr (C::F32) {
 #pragma unroll
                 for (int t = 0; t < 16; ++t) {
@@ -525,6 +530,11 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
                     for (int i = 0; i < D / 32; ++i) dq[i] = mfma_f32(kr[32 * i], s[t], dq[i]);
                 }
             } else {
+                // K^T operand straight from the row-major K tile: lane (d, h)
+                // takes keys 16 ks + {4h .. 4h+3, 8+4h .. 8+4h+3}, the keys of
+                // its dS^T values
+                const int trow = 4 * hi + ((lane & 15) >> 2);
+                const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
                 for (int ks = 0; ks < BN / 16; ++ks) {
                     float ts[8];
@@ -533,25 +543,22 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
                     const s16x8 bs8 = pack8<T>(ts);
 #pragma unroll
                     for (int i = 0; i < D / 32; ++i) {
-                        const s16x8 a = *reinterpret_cast<const s16x8*>(KT + (32 * i + l32) * TW + 16 * ks + 8 * hi);
+                        const T* kp = Ks + (16 * ks + trow) * KW + 32 * i + tcol;
+                        const s16x8 a = cat4(lds_read_tr16(kp), lds_read_tr16(kp + 8 * KW));
                         dq[i] = Elem<T>::mfma(a, bs8, dq[i]);
                     }
                 }
             }
         }
-        if (j + 1 < n_tiles) store_tile((j + 1) & 1);
+        bcur = nxt(bcur);
     };
 
-    if (n_tiles > 0) {
-        load_tile(0);
-        store_tile(0);
-    }
     for (int j = 0; j < n_plain; ++j) step(j, std::false_type{});
     for (int j = n_plain; j < n_tiles; ++j) step(j, std::true_type{});
 
-    lds_barrier();
+    sync_tiles();  // no copy in flight, all waves done with the tiles
     constexpr int OW = C::OW;
-    T* Os = smem + w * 32 * OW;
+    T* Os = (T*)smem + w * 32 * OW;
 #pragma unroll
     for (int i = 0; i < D / 32; ++i)
 #pragma unroll
