@@ -167,99 +167,7 @@ __device__ FA_INLINE inline __amdgpu_buffer_rsrc_t row_buffer(const T* base, int
 // not re-wait for them (together with the next tile's prefetch) each iteration.
 __device__ FA_INLINE inline void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
-__device__ FA_INLINE inline uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, int byte_offset) {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 0));
-}
-
 // ---------------------------------------------------------------------------
-// Row permutation used by transposed LDS tiles.  The MFMA accumulator of
-// lane l holds rows {8(r/4) + 4(l/32) + r%4}; when those rows become the
-// contraction (k) index of a later product, the 8 k-values lane l supplies are
-// rows 16s + {4h .. 4h+3, 8+4h .. 8+4h+3} (h = l/32).  Storing row r at column
-// slot(r) = r with bits 2 and 3 swapped makes those 8 rows contiguous
-// (slots 16s + 8h .. 16s + 8h + 7), so one ds_read_b128 fetches the operand.
-__device__ FA_INLINE inline int slot_of_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
-
-// Global -> register -> LDS staging of a [R][D] tile of 16-bit elements.
-// Each thread owns units of 4 rows x 8 columns (four 16-byte loads) and can
-// write them to LDS row-major (store_rows) and/or transposed with the row
-// permutation above (store_trans: XT[d][slot_of_row(r)] = X[r][d], one
-// ds_write_b64 per column after a byte-permute of the four rows).
-//
-// Unit -> lane mapping (RG = R/4 row groups, CG = D/8 column groups):
-//  * ROWS_FAST = false: row group rg = 4 * (u / (4 * CG)) + u % 4, column
-//    group cg = (u / 4) % CG.  Each load instruction of a wave covers whole
-//    rows, and 16 consecutive lanes of a row store cover all 64 LDS banks.
-//  * ROWS_FAST = true (for store_trans): rg = u % RG, cg = u / RG.  One
-//    transposed store instruction then writes rows 8cg + j of only four
-//    column groups, at 16 distinct slot offsets each; with the other mapping
-//    the 16 column groups of one instruction write rows 8 apart, and rows 16
-//    apart share banks for every 16-byte-aligned row stride.
-template <typename T, int R, int D, int NT, bool ROWS_FAST = false>
-struct Tile16 {
-    static_assert(sizeof(T) == 2, "16-bit elements only");
-    static_assert(R % 16 == 0 && D % 8 == 0, "tile shape");
-    static constexpr int CG = D / 8;
-    static constexpr int RG = R / 4;
-    static constexpr int UNITS = RG * CG;
-    static constexpr int PER = (UNITS + NT - 1) / NT;
-    uint4 r[PER][4];
-
-    __device__ FA_INLINE static inline int row_group(int u) { return ROWS_FAST ? u % RG : 4 * ((u >> 2) / CG) + (u & 3); }
-    __device__ FA_INLINE static inline int col_group(int u) { return ROWS_FAST ? u / RG : (u >> 2) % CG; }
-
-    // Rows >= nvalid read as zeros (buffer range check); no branches or
-    // selects on the loaded data, so nothing forces an early wait on the loads.
-    __device__ FA_INLINE inline void load(const T* __restrict__ base, int64_t row_stride, int nvalid, int tid) {
-        const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D>(base, row_stride, nvalid);
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int u = tid + i * NT;
-            if (UNITS % NT == 0 || u < UNITS) {
-                const int rg = row_group(u), cg = col_group(u);
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    r[i][k] = buffer_load16(rs, (int)(((4 * rg + k) * row_stride + 8 * cg) * (int64_t)sizeof(T)));
-            }
-        }
-    }
-    template <int W>
-    __device__ FA_INLINE inline void store_rows(T* lds, int tid) const {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int u = tid + i * NT;
-            if (UNITS % NT == 0 || u < UNITS) {
-                const int rg = row_group(u), cg = col_group(u);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) *reinterpret_cast<uint4*>(lds + (4 * rg + k) * W + 8 * cg) = r[i][k];
-            }
-        }
-    }
-    template <int W>
-    __device__ FA_INLINE inline void store_trans(T* ldsT, int tid) const {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int u = tid + i * NT;
-            if (UNITS % NT == 0 || u < UNITS) {
-                const int rg = row_group(u), cg = col_group(u);
-                const int s0 = slot_of_row(4 * rg);
-                const uint32_t* a = reinterpret_cast<const uint32_t*>(&r[i][0]);
-                const uint32_t* b = reinterpret_cast<const uint32_t*>(&r[i][1]);
-                const uint32_t* c = reinterpret_cast<const uint32_t*>(&r[i][2]);
-                const uint32_t* d = reinterpret_cast<const uint32_t*>(&r[i][3]);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-                    uint2 v;
-                    v.x = __builtin_amdgcn_perm(b[j >> 1], a[j >> 1], sel);  // rows 0,1 of column j
-                    v.y = __builtin_amdgcn_perm(d[j >> 1], c[j >> 1], sel);  // rows 2,3
-                    *reinterpret_cast<uint2*>(ldsT + (8 * cg + j) * W + s0) = v;
-                }
-            }
-        }
-    }
-};
-
 // One 16-byte-per-lane global -> LDS load (buffer_load_dwordx4 ... lds): lane
 // l writes LDS bytes [16 l, 16 l + 16) past `lds`, which must be wave-uniform.
 // A function of its own: written directly in the kernel templates, the
@@ -359,38 +267,5 @@ template <typename T>
 __device__ FA_INLINE inline void dma_load4(__amdgpu_buffer_rsrc_t rs, T* lds, int byte_offset) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 4, byte_offset, 0, 0, 0);
 }
-
-// ---------------------------------------------------------------------------
-// Global -> register -> LDS staging of a [ROWS][D] tile of T with 16-byte
-// chunks (LDS row stride LDSW elements); same tail handling as Tile16.
-template <typename T, int ROWS, int D, int NT>
-struct TileStage {
-    static constexpr int EPC = 16 / sizeof(T);  // elements per 16-byte chunk
-    static constexpr int CPR = D / EPC;         // chunks per row
-    static constexpr int TOTAL = ROWS * CPR;
-    static constexpr int PER = (TOTAL + NT - 1) / NT;
-    uint4 r[PER];
-
-    __device__ FA_INLINE inline void load(const T* __restrict__ base, int64_t row_stride, int nvalid, int tid) {
-        const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D>(base, row_stride, nvalid);
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int c = tid + i * NT;
-            const int row = c / CPR, col = c % CPR;
-            if (TOTAL % NT == 0 || c < TOTAL)
-                r[i] = buffer_load16(rs, (int)((row * row_stride + col * EPC) * (int64_t)sizeof(T)));
-        }
-    }
-    template <int LDSW>
-    __device__ FA_INLINE inline void store(T* lds, int tid) const {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int c = tid + i * NT;
-            const int row = c / CPR, col = c % CPR;
-            if (TOTAL % NT == 0 || c < TOTAL)
-                *reinterpret_cast<uint4*>(lds + row * LDSW + col * EPC) = r[i];
-        }
-    }
-};
 
 }  // namespace fa

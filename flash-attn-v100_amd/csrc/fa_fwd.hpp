@@ -9,9 +9,11 @@
 // accumulator is lane-aligned with the softmax statistics (rescale is lane-local).
 //   * Q lives in registers for the whole KV loop (MFMA B operand).
 //   * K/V tiles stream through double-buffered LDS (one barrier per tile),
-//     loaded with 16-byte global loads issued a full tile ahead.
-//   * V is written to LDS transposed (V^T[d][slot(key)], key order permuted to
-//     match the P accumulator layout), so PV operands are single ds_read_b128.
+//     copied global -> LDS directly (buffer_load ... lds) a full tile ahead.
+//   * PV operands (V^T fragments) are read from the row-major V tile with
+//     ds_read_b64_tr_b16, in the key order of the P accumulator layout.
+//   * the loop is software-pipelined: S of the next tile is issued alongside
+//     the softmax of the current one.
 //   * exp2 with scale*log2(e) folded into one FMA; the running max is only
 //     moved (and O rescaled) when it grows by more than 2^8, which is exact.
 //   * causal: KV tiles past the last query are never loaded; tiles past a
@@ -36,10 +38,11 @@ struct FwdCfg {
     static constexpr int BN = F32 ? 32 : 64;      // keys per tile
     static constexpr int NB = BN / 32;            // 32-key blocks per tile
     static constexpr int KW = D + (F32 ? 4 : 8);  // K row stride (elements)
-    // V: fp32 keeps rows (stride D + 8); 16-bit types store V^T[d][slot(key)]
-    static constexpr int VW = F32 ? D + 8 : BN + 8;
+    // V rows; 16-bit types read V^T fragments with ds_read_b64_tr_b16, whose
+    // four rows per lane group fall in distinct banks at this stride
+    static constexpr int VW = F32 ? D + 8 : D + (D == 64 ? 8 : 24);
     static constexpr int KTILE = BN * KW;
-    static constexpr int VTILE = F32 ? BN * VW : D * VW;
+    static constexpr int VTILE = BN * VW;
     static constexpr int OW = D + (F32 ? 4 : 8);  // output staging row stride
     static constexpr int SMEM_ELEMS = 2 * (KTILE + VTILE);
     static_assert(NW * 32 * OW <= SMEM_ELEMS, "O staging must fit in the K/V buffers");
@@ -101,8 +104,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
 
     T* Ks0 = smem;
     T* Vs0 = smem + 2 * C::KTILE;
-    // K tiles (and fp32 V tiles, kept row-major) go global -> LDS directly;
-    // 16-bit V tiles are staged through registers and stored transposed.
+    // K and V tiles go global -> LDS directly and stay row-major.
     // Loads past the last key read as zeros (buffer range check), so the
     // pipeline below issues them unconditionally; such tiles are never used.
     const int wv = __builtin_amdgcn_readfirstlane(w);
@@ -111,16 +113,10 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     auto dma_k = [&](int j, int slot) {
         kdma.load(kbase + (int64_t)(j * BN) * p.k_ss, p.k_ss, p.Sk - j * BN, Ks0 + slot * C::KTILE, lane);
     };
-    using VStage = typename std::conditional<C::F32, DmaTile<T, BN, D, VW, C::NW>, Tile16<T, BN, D, C::NT, true>>::type;
-    VStage vst;
-    if constexpr (C::F32) vst.init(p.v_ss, lane, wv);
-    // 16-bit: load V(j) into registers; fp32: copy V(j) into V slot `slot`
+    DmaTile<T, BN, D, VW, C::NW> vst;
+    vst.init(p.v_ss, lane, wv);
     auto load_v = [&](int j, int slot) {
-        if constexpr (C::F32) vst.load(vbase + (int64_t)(j * BN) * p.v_ss, p.v_ss, p.Sk - j * BN, Vs0 + slot * C::VTILE, lane);
-        else vst.load(vbase + (int64_t)(j * BN) * p.v_ss, p.v_ss, p.Sk - j * BN, tid);
-    };
-    auto store_v = [&](int slot) {
-        if constexpr (!C::F32) vst.template store_trans<VW>(Vs0 + slot * C::VTILE, tid);
+        vst.load(vbase + (int64_t)(j * BN) * p.v_ss, p.v_ss, p.Sk - j * BN, Vs0 + slot * C::VTILE, lane);
     };
 
     // ---- S^T = K Q^T for one key tile ----
@@ -229,25 +225,26 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
             for (int ks = 0; ks < BN / 16; ++ks)
 #pragma unroll
                 for (int i = 0; i < D / 32; ++i) {
-                    const s16x8 a = *reinterpret_cast<const s16x8*>(Vs + (32 * i + l32) * VW + 16 * ks + 8 * hi);
+                    // V^T fragment from the row-major tile: lane (d, h) takes keys
+                    // 16 ks + {4h .. 4h+3, 8+4h .. 8+4h+3}, the keys of its P^T values
+                    const T* vp = Vs + (16 * ks + 4 * hi + ((lane & 15) >> 2)) * VW + 32 * i + 16 * ((lane >> 4) & 1) +
+                                  4 * (lane & 3);
+                    const s16x8 a = cat4(lds_read_tr16(vp), lds_read_tr16(vp + 8 * VW));
                     o[i] = Elem<T>::mfma(a, pk[ks], o[i]);
                 }
         }
     };
 
     // Software pipeline over key tiles.  Iteration j issues the MFMAs of
-    // S(j+1) together with the softmax of S(j) (VALU) and the LDS store of the
-    // staged V tile, then P(j) V(j) together with the max of S(j+1) and the
-    // loads of the next tiles, so that the matrix pipe, the VALU, LDS and the
-    // memory pipe overlap inside one wave.
+    // S(j+1) together with the softmax of S(j) (VALU), then P(j) V(j)
+    // together with the max of S(j+1), so that the matrix pipe and the VALU
+    // overlap inside one wave.
     //
     // LDS holds two K slots and two V slots.  Iteration j reads K(j+1) from
-    // K slot (j+1)&1 and V(j) from V slot j&1.  It copies K(j+2) into K slot
-    // j&1 and (16-bit) stores the registers holding V(j+1) into V slot
-    // (j+1)&1 -- both slots were last read in iteration j-1, which every wave
-    // finished before the barrier that opens iteration j -- and then loads
-    // V(j+2) into the registers (fp32: copies V(j+1) into its slot directly).
-    // Direct-to-LDS copies complete when the issuing wave's vmcnt drains, so
+    // K slot (j+1)&1 and V(j) from V slot j&1, and copies K(j+2) into K slot
+    // j&1 and V(j+1) into V slot (j+1)&1 -- both slots were last read in
+    // iteration j-1, which every wave finished before the barrier that opens
+    // iteration j.  Direct-to-LDS copies complete when the issuing wave's vmcnt drains, so
     // every barrier that publishes tiles is preceded by a wait for all of the
     // wave's outstanding loads (sync_tiles); the compiler only orders them
     // against the wave's own LDS reads.
@@ -267,8 +264,6 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
         dma_k(0, 0);
         dma_k(1, 1);
         load_v(0, 0);
-        store_v(0);
-        if constexpr (!C::F32) load_v(1, 1);
     }
     sync_tiles();
     if (n_w > 0) {
@@ -281,15 +276,13 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
         constexpr bool MASK = decltype(mask_tag)::value;
         sync_tiles();
         dma_k(j + 2, j & 1);
-        if constexpr (C::F32) load_v(j + 1, (j + 1) & 1);
+        load_v(j + 1, (j + 1) & 1);
         const bool act = !MASK || j < n_w;
         const bool next = !MASK || j + 1 < n_w;
         if (act) {
             if (next) qk(Ks0 + ((j + 1) & 1) * C::KTILE, sn);
             softmax(sc, pk, j * BN);
         }
-        store_v((j + 1) & 1);
-        if constexpr (!C::F32) load_v(j + 2, 0);
         if (act) pv(Vs0 + (j & 1) * C::VTILE, sc, pk);
         if (act && next) {
             if (MASK) mask(sn, (j + 1) * BN);
