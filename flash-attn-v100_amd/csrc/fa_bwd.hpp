@@ -1,20 +1,21 @@
 // FlashAttention backward for gfx950 (reference: kernels/backward_kernel.py:17-205,
 // whose racy low-precision dQ read-modify-write and per-tile-pair delta are
 // replaced).  Three deterministic kernels, no atomics:
-//   1. delta_kernel: delta = rowsum(dO * O) in fp32, (B, H, Sq).
+//   1. delta_kernel: LSE * log2 e and delta = rowsum(dO * O) in fp32 into the
+//      workspace rows.
 //   2. dkdv_kernel: one workgroup per 128 keys of one (batch, KV head); wave w
 //      owns keys k0 + 32w .. +31 (lane l owns key k0 + 32w + l%32), K and V rows
-//      stay in registers; 32-query tiles of Q, dO, LSE, delta stream through
-//      double-buffered LDS.  Scores are computed as S = Q K^T so each lane holds
-//      queries {8(r/4) + 4(l/32) + r%4} of ITS key, which is exactly the MFMA
+//      stay in registers; 64-query tiles of Q, dO and the LSE / delta rows are
+//      copied global -> LDS (double-buffered) and consumed as two 32-query
+//      sub-steps.  Scores are computed as S = Q K^T so each lane holds queries
+//      {8(r/4) + 4(l/32) + r%4} of ITS key, which is exactly the MFMA
 //      B-operand layout needed for dV^T = dO^T P and dK^T = Q^T dS (the dO^T /
-//      Q^T operands come from the row-major LDS tiles via ds_read_b64_tr_b16;
-//      a second, transposed copy of the tiles measured slower here).
+//      Q^T operands come from the row-major LDS tiles via ds_read_b64_tr_b16).
 //      Query heads sharing a KV head are summed in-register.
 //   3. dq_kernel: one workgroup per 128 queries of one (batch, head), like the
 //      forward: S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T with Q, dO, LSE,
-//      delta held per lane; K/V tiles stream through double-buffered LDS (K
-//      both row-major and transposed).
+//      delta held per lane; K/V tiles are copied global -> LDS into three
+//      rotating buffers, K^T read from the K tile with transposing reads.
 // Diagonal (causal) tiles run a separate masking variant of each tile step.
 // All five products accumulate in fp32 and are rounded once to the input dtype.
 #pragma once
@@ -78,18 +79,19 @@ struct DkdvCfg {
     static constexpr int NW = 4;
     static constexpr int NT = 64 * NW;
     static constexpr int BK = 32 * NW;              // keys per workgroup
-    static constexpr int BQ = 32;                   // queries per tile
+    static constexpr int NSUB = 2;                  // 32-query sub-tiles per tile
+    static constexpr int BQ = 32 * NSUB;            // queries per tile
     // Q / dO row stride: odd multiple of 16 bytes (conflict-free ds_read_b128
     // row reads) whose 4 consecutive rows of a ds_read_b64_tr_b16 do not overlap
     // in the 256-byte bank window
     static constexpr int RW = D + (F32 ? 4 : (D == 64 ? 8 : 24));
     static constexpr int QTILE = BQ * RW;
     // Q (waves 0-1) and dO (waves 2-3) tiles are copied global -> LDS directly
-    using Rows = DmaRows<T, BQ, D, RW, NW / 2>;
-    static constexpr int QALLOC = Rows::LDS_BYTES;  // tile + copy slack
+    using Rows = DmaRowGroups<T, BQ, D, RW, NW / 2>;
+    static constexpr int QALLOC = BQ * RW * (int)sizeof(T);
     // per buffer: Q rows, dO rows, then LSE * log2 e [BQ] and delta [BQ] as floats
     static constexpr int BUF_BYTES = 2 * QALLOC + 2 * BQ * 4;
-    static constexpr int NBUF = 3;                  // tiles t, t+1 read while t+2 lands
+    static constexpr int NBUF = 2;                  // tile t read while t+1 lands
     static constexpr int OW = D + (F32 ? 4 : 8);    // output staging stride
     static constexpr int SMEM_BYTES_RAW = NBUF * BUF_BYTES;
     static constexpr int STAGE_BYTES = NW * 32 * OW * (int)sizeof(T);
@@ -150,33 +152,22 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
     const bool copy_q = w < C::NW / 2;
     typename C::Rows rows;
     rows.init(copy_q ? p.q_ss : p.do_ss, lane, w % (C::NW / 2));
-    const int ws_lane = 4 * (lane < BQ ? lane : p.sq_pad + lane - BQ);
-    static_assert(2 * BQ == 64, "one dword per lane for LSE and delta");
+    static_assert(BQ == 64, "one dword per lane for each of LSE and delta");
     auto buf = [&](int s) -> char* { return smem + s * C::BUF_BYTES; };
     auto tile_head = [&](int it) { return hk * p.group + it / nq; };
     auto tile_q0 = [&](int it) { return (qt_begin + it % nq) * BQ; };
-    // copy of tile `it` into buffer s, in three parts (PART 2 also copies the
-    // LSE / delta row) so that they can be spread between MFMAs
-    constexpr int P3 = (C::Rows::PER + 2) / 3;
-    auto issue = [&](int it, int s, auto part_tag) FA_INLINE {
-        constexpr int PART = decltype(part_tag)::value;
+    auto issue = [&](int it, int s) FA_INLINE {
         const int hh = tile_head(it), qb0 = tile_q0(it);
         char* bp = buf(s);
         const T* src = copy_q ? (const T*)p.q + b * p.q_sb + (int64_t)qb0 * p.q_ss + hh * p.q_sh
                               : (const T*)p.dout + b * p.do_sb + (int64_t)qb0 * p.do_ss + hh * p.do_sh;
-        rows.template load<PART * P3, (PART + 1) * P3>(src, copy_q ? p.q_ss : p.do_ss, p.Sq - qb0,
-                                                        (T*)(bp + (copy_q ? 0 : C::QALLOC)));
-        if constexpr (PART == 2) {
-            const float* wrow = p.lse2 + ((int64_t)b * p.H + hh) * p.ws_stride + qb0;  // qb0 + BQ <= sq_pad
-            const __amdgpu_buffer_rsrc_t rs =
-                __builtin_amdgcn_make_buffer_rsrc((void*)wrow, (short)0, (p.ws_stride - qb0) * 4, 0x00020000);
-            dma_load4(rs, bp + 2 * C::QALLOC, ws_lane);
-        }
-    };
-    auto issue_all = [&](int it, int s) FA_INLINE {
-        issue(it, s, std::integral_constant<int, 0>{});
-        issue(it, s, std::integral_constant<int, 1>{});
-        issue(it, s, std::integral_constant<int, 2>{});
+        rows.load(src, copy_q ? p.q_ss : p.do_ss, p.Sq - qb0, (T*)(bp + (copy_q ? 0 : C::QALLOC)));
+        const float* wrow = p.lse2 + ((int64_t)b * p.H + hh) * p.ws_stride + qb0;  // qb0 + BQ <= sq_pad
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc((void*)wrow, (short)0, (p.ws_stride - qb0) * 4, 0x00020000);
+        float* f = (float*)(bp + 2 * C::QALLOC);
+        dma_load4(rs, f, 4 * lane);                 // LSE * log2 e
+        dma_load4(rs, f + BQ, 4 * (p.sq_pad + lane));  // delta
     };
     // direct-to-LDS copies complete when the issuing wave's vmcnt drains
     auto sync_tiles = [&]() {
@@ -185,19 +176,16 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
     };
 
     // ---- S = Q K^T and dP = dO V^T for the tile in buffer s (C[q][key]) ----
-    auto sdp = [&](int s, f32x16& sc, f32x16& dpc, auto lo_tag, auto hi_tag) FA_INLINE {
-        constexpr int LO = decltype(lo_tag)::value, HI = decltype(hi_tag)::value;
+    auto sdp = [&](int s, int st, f32x16& sc, f32x16& dpc) FA_INLINE {
         const T* Qs = (const T*)buf(s);
         const T* Ds = (const T*)(buf(s) + C::QALLOC);
-        if constexpr (LO == 0) {
-            sc = f32x16{};
-            dpc = f32x16{};
-        }
-        const T* qrow = Qs + l32 * RW;
-        const T* drow = Ds + l32 * RW;
+        sc = f32x16{};
+        dpc = f32x16{};
+        const T* qrow = Qs + (32 * st + l32) * RW;
+        const T* drow = Ds + (32 * st + l32) * RW;
         if constexpr (C::F32) {
 #pragma unroll
-            for (int i = LO; i < HI; ++i) {
+            for (int i = 0; i < KR; ++i) {
                 const f32x4 aq = *reinterpret_cast<const f32x4*>(qrow + hi * (D / 2) + 4 * i);
                 const f32x4 ad = *reinterpret_cast<const f32x4*>(drow + hi * (D / 2) + 4 * i);
                 const f32x4 bk = __builtin_bit_cast(f32x4, kreg[i]);
@@ -210,7 +198,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
             }
         } else {
 #pragma unroll
-            for (int kk = LO; kk < HI; ++kk) {
+            for (int kk = 0; kk < KR; ++kk) {
                 const s16x8 aq = *reinterpret_cast<const s16x8*>(qrow + 16 * kk + 8 * hi);
                 const s16x8 ad = *reinterpret_cast<const s16x8*>(drow + 16 * kk + 8 * hi);
                 sc = Elem<T>::mfma(aq, __builtin_bit_cast(s16x8, kreg[kk]), sc);
@@ -220,14 +208,14 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
     };
 
     // ---- P and dS of tile `it` (buffer s); dS = P (dP - delta), scale applied at the end ----
-    constexpr int NPK = C::F32 ? 1 : BQ / 16;
+    constexpr int NPK = C::F32 ? 1 : 2;
     float pd[16], ds[16];
     s16x8 bp8[NPK], bs8[NPK];
-    auto softmax_ds = [&](int it, int s, const f32x16& sc, const f32x16& dpc, auto mask_tag) FA_INLINE {
+    auto softmax_ds = [&](int it, int s, int st, const f32x16& sc, const f32x16& dpc, auto mask_tag) FA_INLINE {
         constexpr bool MASK = decltype(mask_tag)::value;
-        const float* lse2 = (const float*)(buf(s) + 2 * C::QALLOC);
+        const float* lse2 = (const float*)(buf(s) + 2 * C::QALLOC) + 32 * st;
         const float* dels = lse2 + BQ;
-        const int qb0 = tile_q0(it);
+        const int qb0 = tile_q0(it) + 32 * st;
         uint64_t col_ctr = 0;
         if (DROPOUT)
             col_ctr = p.offset + (uint64_t)(b * p.H + tile_head(it)) * (uint64_t)p.Sq * (uint64_t)p.Sk + (uint64_t)kj;
@@ -255,7 +243,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
         }
         if constexpr (!C::F32) {
 #pragma unroll
-            for (int ks = 0; ks < BQ / 16; ++ks) {
+            for (int ks = 0; ks < 2; ++ks) {
                 bp8[ks] = pack8<T>(pd + 8 * ks);
                 bs8[ks] = pack8<T>(ds + 8 * ks);
             }
@@ -264,10 +252,10 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
 
     // ---- dV^T += dO^T P,  dK^T += Q^T dS for the tile in buffer s ----
     // half H (0 or 1) of the products: query rows [16 H, 16 H + 16)
-    auto dkdv_acc = [&](int s, auto half_tag) FA_INLINE {
+    auto dkdv_acc = [&](int s, int st, auto half_tag) FA_INLINE {
         constexpr int H2 = decltype(half_tag)::value;
-        const T* Qs = (const T*)buf(s);
-        const T* Ds = (const T*)(buf(s) + C::QALLOC);
+        const T* Qs = (const T*)buf(s) + 32 * st * RW;
+        const T* Ds = (const T*)(buf(s) + C::QALLOC) + 32 * st * RW;
         if constexpr (C::F32) {
 #pragma unroll
             for (int t = 8 * H2; t < 8 * H2 + 8; ++t) {
@@ -282,7 +270,6 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
             // dO^T / Q^T operands straight from the row-major tiles
             const int trow = 4 * hi + ((lane & 15) >> 2);
             const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-            static_assert(BQ == 32, "two 16-query halves");
             constexpr int ks = H2;
 #pragma unroll
                 for (int i = 0; i < D / 32; ++i) {
@@ -295,31 +282,29 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
         }
     };
 
-    // Loop over query tiles.  Three LDS buffers rotate: iteration `it` reads
-    // tile it (buffer it%3) while the copies of tiles it+1 and it+2 are in
-    // flight; tile it+2 goes into the buffer of tile it-1, which every wave
-    // finished before the opening barrier.  Past the last tile the copies
-    // repeat it, which keeps the loop body free of branches.  Two workgroups
-    // share a CU (255 registers per lane), so each SIMD interleaves the
-    // MFMA, softmax and LDS phases of two waves.
+    // Loop over query tiles of 64 (two 32-query sub-steps per barrier).  Two
+    // LDS buffers alternate: iteration `it` reads tile it (buffer it&1) and
+    // copies tile it+1 into the other buffer, last read in iteration it-1,
+    // which every wave finished before the opening barrier.  Past the last
+    // tile the copy repeats it, which keeps the loop body free of branches.
+    // Two workgroups share a CU (255 registers per lane), so each SIMD
+    // interleaves the MFMA, softmax and LDS phases of two waves.
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    using IK = std::integral_constant<int, KR>;
-    if (total > 0) {
-        issue_all(0, 0);
-        issue_all(min(1, total - 1), 1);
-    }
+    if (total > 0) issue(0, 0);
     f32x16 sc, dpc;
-    int bcur = 0;  // it % 3
-    auto nxt = [](int s) { return s == 2 ? 0 : s + 1; };
+    int bcur = 0;  // it & 1
     auto iter = [&](int it, auto mask_tag) FA_INLINE {
         sync_tiles();
-        issue_all(min(it + 2, total - 1), nxt(nxt(bcur)));
-        sdp(bcur, sc, dpc, I0{}, IK{});
-        softmax_ds(it, bcur, sc, dpc, mask_tag);
-        dkdv_acc(bcur, I0{});
-        dkdv_acc(bcur, I1{});
-        bcur = nxt(bcur);
+        issue(min(it + 1, total - 1), bcur ^ 1);
+#pragma unroll
+        for (int st = 0; st < C::NSUB; ++st) {
+            sdp(bcur, st, sc, dpc);
+            softmax_ds(it, bcur, st, sc, dpc, mask_tag);
+            dkdv_acc(bcur, st, I0{});
+            dkdv_acc(bcur, st, I1{});
+        }
+        bcur ^= 1;
     };
     // masked tiles first for each query head of the group, then plain ones
     int it = 0;

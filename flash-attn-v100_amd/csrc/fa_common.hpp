@@ -261,6 +261,44 @@ struct DmaRows {
     }
 };
 
+// Direct global -> LDS copy of a [R][D] tile where each wave instruction
+// copies KR = 64 / CW whole LDS rows (lanes >= KR * CW idle): the lane's
+// global offset is the same for every instruction up to a scalar row step, so
+// the copy keeps one offset register per lane instead of one per instruction.
+// Instructions t = wave, wave + NWAVES, ... (wave-uniform check) cover the
+// tile's row groups; rows >= nvalid land as zeros.
+template <typename T, int R, int D, int W, int NWAVES>
+struct DmaRowGroups {
+    static constexpr int EPC = 16 / (int)sizeof(T);
+    static constexpr int CD = D / EPC;
+    static constexpr int CW = W / EPC;
+    static_assert(D % EPC == 0 && W % EPC == 0 && W >= D && CW <= 64, "16-byte chunked rows");
+    static constexpr int KR = 64 / CW;              // rows per instruction
+    static constexpr int NI = (R + KR - 1) / KR;    // instructions per tile
+    static constexpr int PER = (NI + NWAVES - 1) / NWAVES;
+    int off;   // byte offset of this lane's chunk within its row group
+    int rowl;  // this lane's row within the group (KR for idle lanes)
+    int wave;
+
+    __device__ FA_INLINE inline void init(int64_t row_stride, int lane, int wave_id) {
+        wave = wave_id;
+        rowl = lane < KR * CW ? lane / CW : KR;
+        const int col = min(lane % CW, CD - 1);
+        off = ((lane / CW) * (int)row_stride + col * EPC) * (int)sizeof(T);
+    }
+    __device__ FA_INLINE inline void load(const T* base, int64_t row_stride, int nvalid, T* lds) const {
+        const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D>(base, row_stride, nvalid);
+#pragma unroll
+        for (int t = 0; t < PER; ++t) {
+            const int g = wave + NWAVES * t;
+            // lanes past the KR rows of the group, and (last group) past row R, idle
+            const int rows_here = (R % KR == 0 || g < NI - 1) ? KR : R - (NI - 1) * KR;
+            if ((NI % NWAVES == 0 || g < NI) && rowl < rows_here)
+                dma_load16(rs, lds + g * KR * W, off + g * KR * (int)row_stride * (int)sizeof(T));
+        }
+    }
+};
+
 // One dword per lane global -> LDS (buffer_load_dword ... lds): lane l writes
 // LDS bytes [4 l, 4 l + 4) past `lds` (wave-uniform).
 template <typename T>
