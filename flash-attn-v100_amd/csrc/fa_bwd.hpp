@@ -14,8 +14,9 @@
 //      Query heads sharing a KV head are summed in-register.
 //   3. dq_kernel: one workgroup per 128 queries of one (batch, head), like the
 //      forward: S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T with Q, dO, LSE,
-//      delta held per lane; K/V tiles are copied global -> LDS into three
-//      rotating buffers, K^T read from the K tile with transposing reads.
+//      delta held per lane; 64-key K/V tiles are copied global -> LDS
+//      (double-buffered) and consumed as two 32-key sub-steps, K^T read from
+//      the K tile with transposing reads.
 // Diagonal (causal) tiles run a separate masking variant of each tile step.
 // All five products accumulate in fp32 and are rounded once to the input dtype.
 #pragma once
@@ -363,15 +364,16 @@ struct DqCfg {
     static constexpr int NW = 4;
     static constexpr int NT = 64 * NW;
     static constexpr int BM = 32 * NW;            // queries per workgroup
-    static constexpr int BN = 32;                 // keys per tile
+    static constexpr int NSUB = 2;                // 32-key sub-tiles per tile
+    static constexpr int BN = 32 * NSUB;          // keys per tile
     // K / V row stride: conflict-free ds_read_b128 row reads and (16-bit)
     // ds_read_b64_tr_b16 reads of K^T, as for the dK/dV tiles
     static constexpr int KW = D + (F32 ? 4 : (D == 64 ? 8 : 24));
     // K (waves 0-1) and V (waves 2-3) tiles are copied global -> LDS directly
-    using Rows = DmaRows<T, BN, D, KW, NW / 2>;
-    static constexpr int KALLOC = Rows::LDS_BYTES;  // tile + copy slack
+    using Rows = DmaRowGroups<T, BN, D, KW, NW / 2>;
+    static constexpr int KALLOC = BN * KW * (int)sizeof(T);
     static constexpr int BUF_BYTES = 2 * KALLOC;    // K rows, V rows
-    static constexpr int NBUF = 3;
+    static constexpr int NBUF = 2;
     static constexpr int OW = D + (F32 ? 4 : 8);
     static constexpr int STAGE_BYTES = NW * 32 * OW * (int)sizeof(T);
     static constexpr int SMEM_BYTES = NBUF * BUF_BYTES > STAGE_BYTES ? NBUF * BUF_BYTES : STAGE_BYTES;
@@ -446,24 +448,18 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
         lds_barrier();
     };
 
-    // Three LDS buffers rotate: tile j is read from buffer j%3 while tiles
-    // j+1 and j+2 are in flight; tile j+2 goes into the buffer of tile j-1,
-    // which every wave finished before the opening barrier.  Past the last
-    // tile the copies repeat it (never read), so the copy is branch-free.
+    // Two LDS buffers alternate: tile j (64 keys, consumed as two 32-key
+    // sub-steps) is read from buffer j&1 while tile j+1 is copied into the
+    // other buffer, last read in iteration j-1, which every wave finished
+    // before the opening barrier.  Past the last tile the copy repeats it
+    // (never read), so the copy is branch-free.
     int bcur = 0;
-    auto nxt = [](int s) { return s == 2 ? 0 : s + 1; };
-    if (n_tiles > 0) {
-        issue(0, 0);
-        issue(min(1, n_tiles - 1), 1);
-    }
+    if (n_tiles > 0) issue(0, 0);
 
-    auto step = [&](int j, auto mask_tag) FA_INLINE {
+    // one 32-key sub-step of the tile in buffer `bcur` starting at key k0
+    auto sub = [&](int k0, const T* Ks, const T* Vs, auto mask_tag) FA_INLINE {
         constexpr bool MASK = decltype(mask_tag)::value;
-        const int k0 = j * BN;
-        sync_tiles();
-        issue(min(j + 2, n_tiles - 1), nxt(nxt(bcur)));
-        const T* Ks = (const T*)buf(bcur);
-        const T* Vs = (const T*)(buf(bcur) + C::KALLOC);
+        constexpr int BN = 32;
         const bool active = !MASK || !CAUSAL || k0 <= qw0 + 31;
         if (active) {
             // ---- S^T = K Q^T, dP^T = V dO^T (C[key][query]) ----
@@ -535,7 +531,15 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
                 }
             }
         }
-        bcur = nxt(bcur);
+    };
+    auto step = [&](int j, auto mask_tag) FA_INLINE {
+        sync_tiles();
+        issue(min(j + 1, n_tiles - 1), bcur ^ 1);
+#pragma unroll
+        for (int st = 0; st < C::NSUB; ++st)
+            sub(j * C::BN + 32 * st, (const T*)buf(bcur) + 32 * st * KW, (const T*)(buf(bcur) + C::KALLOC) + 32 * st * KW,
+                mask_tag);
+        bcur ^= 1;
     };
 
     for (int j = 0; j < n_plain; ++j) step(j, std::false_type{});
