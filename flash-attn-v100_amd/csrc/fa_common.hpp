@@ -71,10 +71,30 @@ __device__ FA_INLINE inline s16x8 pack8(const float* x) {
     return r;
 }
 
-// value held by lane l^32.  (v_permlane32_swap with both operands equal to x
-// would do this in one VALU op, but the compiler folds the per-half select of
-// its two results to the first one, so the LDS-crossbar shuffle is used.)
-__device__ FA_INLINE inline float swap_halves(float x) { return __shfl_xor(x, 32, 64); }
+// Reductions over the lane pair (l, l^32) with one v_permlane32_swap (no LDS
+// round trip).  Swapping x with itself leaves x[l%32] in one result and
+// x[l%32 + 32] in the other for every lane, so max / sum of the two results is
+// the pair reduction in all 64 lanes without a per-half select.  The second
+// result passes through a register move the compiler cannot see through: it
+// otherwise folds max(r0, r1) and r0 + r1 as if both results were x.
+__device__ FA_INLINE inline void pair_swap(float x, float& a, float& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x),
+                                                    false, false);
+    unsigned hidden;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(hidden) : "v"(r[1]));
+    a = __builtin_bit_cast(float, (unsigned)r[0]);
+    b = __builtin_bit_cast(float, hidden);
+}
+__device__ FA_INLINE inline float pair_max(float x) {
+    float a, b;
+    pair_swap(x, a, b);
+    return fmaxf(a, b);
+}
+__device__ FA_INLINE inline float pair_sum(float x) {
+    float a, b;
+    pair_swap(x, a, b);
+    return a + b;
+}
 
 __device__ FA_INLINE inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

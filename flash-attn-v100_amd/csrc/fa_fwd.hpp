@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
         for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
             for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[blk][r]);
-        mx = fmaxf(mx, swap_halves(mx));
+        mx = pair_max(mx);
         m_raw = fmaxf(m_raw, mx);
         const float m_new = fmaxf(m_run, mx * c);
         if (__ballot(m_new > m_run + 8.0f) != 0ull) {
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     if (j < n_tiles) iter(j, sa, sb, std::true_type{});
 
     // ---- epilogue: normalise, LSE, stage O^T through LDS, coalesced store ----
-    const float l_tot = l_run + swap_halves(l_run);
+    const float l_tot = pair_sum(l_run);
     const float inv = l_tot > 0.f ? (DROPOUT ? p.rp : 1.f) / l_tot : 0.f;
     if (hi == 0 && qi < p.Sq) {
         const int64_t si = (int64_t)(b * p.H + h) * p.Sq + qi;
