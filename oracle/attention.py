@@ -24,13 +24,18 @@ is the textbook math, with
 * causal masks key ``j > i`` (top-left aligned, ``forward_kernel.py:181``,
   ``tests/test_attention.py:63``), also when Sq != Sk;
 * grouped KV heads: query head ``h`` reads KV head ``h // (H // Hkv)``
-  (``utils.py:88-97`` allows ``H % Hkv == 0``).
+  (``utils.py:88-97`` allows ``H % Hkv == 0``);
+* an optional additive bias of shape (B|1, H|1, Sq, Sk) is added to the scaled
+  scores before the causal mask (``forward_kernel.py:166-182``: ``qk * scale``,
+  ``+ bias_block``, then ``tl.where(causal_mask, qk, -inf)``).
 
 Gradients follow ``kernels/backward_kernel.py:118-176`` with the row index of
 the dropout counter and the saved dropout mask restored:
 ``delta_i = sum_d dO_id O_id``, ``dP = (dO V^T) * Z/(1-p)``,
 ``dS = P * (dP - delta)``, ``dV = (P * Z/(1-p))^T dO``, ``dK = scale dS^T Q``,
-``dQ = scale dS K``.
+``dQ = scale dS K``.  The bias gradient is ``dS`` itself (the gradient of the
+biased scores), summed over the dimensions the bias broadcasts; the reference
+returned zeros for it (``ops/attention.py:297-301``).
 """
 from __future__ import annotations
 
@@ -45,6 +50,7 @@ __all__ = [
     "attention_backward",
     "attention_autograd",
     "brute_force_forward",
+    "reduce_to_bias_shape",
     "flops",
 ]
 
@@ -70,10 +76,12 @@ def _causal_mask(sq: int, sk: int, device=None) -> torch.Tensor:
     return torch.triu(torch.ones(sq, sk, dtype=torch.bool, device=device), diagonal=1)
 
 
-def _scores(q, k, causal, scale, dtype):
+def _scores(q, k, causal, scale, dtype, bias=None):
     qh = q.to(dtype).transpose(1, 2)  # (B, H, Sq, D)
     kh = k.to(dtype).transpose(1, 2)
     s = torch.matmul(qh, kh.transpose(-2, -1)) * scale
+    if bias is not None:
+        s = s + bias.to(dtype)  # broadcasts over B and H
     if causal:
         s = s.masked_fill(_causal_mask(s.shape[-2], s.shape[-1], s.device), float("-inf"))
     return s
@@ -88,10 +96,12 @@ def attention_forward(
     dropout_mask: Optional[torch.Tensor] = None,
     dropout_p: float = 0.0,
     dtype: torch.dtype = torch.float64,
+    bias: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Forward O (B, Sq, H, D) in ``dtype`` and LSE (B, H, Sq) in ``dtype``.
 
-    ``dropout_mask`` is a bool keep-mask (B, H, Sq, Sk) or None.
+    ``dropout_mask`` is a bool keep-mask (B, H, Sq, Sk) or None; ``bias`` an
+    additive (B|1, H|1, Sq, Sk) tensor or None.
     Rows with no unmasked key (only possible when Sk == 0) give O = 0 and
     LSE = -inf.
     """
@@ -104,7 +114,7 @@ def attention_forward(
     if Sk == 0:
         return (torch.zeros(B, Sq, H, D, dtype=dtype, device=q.device),
                 torch.full((B, H, Sq), float("-inf"), dtype=dtype, device=q.device))
-    s = _scores(q, k, causal, scale, dtype)
+    s = _scores(q, k, causal, scale, dtype, bias)
     lse = torch.logsumexp(s, dim=-1)
     p = torch.exp(s - lse.unsqueeze(-1))
     if dropout_p > 0.0:
@@ -122,16 +132,18 @@ def attention_backward(
     dropout_mask: Optional[torch.Tensor] = None,
     dropout_p: float = 0.0,
     dtype: torch.dtype = torch.float64,
+    bias: Optional[torch.Tensor] = None,
 ):
     """Explicit-formula backward (dQ, dK, dV) in ``dtype``; dK/dV summed over
-    the query heads that share a KV head."""
+    the query heads that share a KV head.  With ``bias`` also returns dBias
+    (the bias's shape) as a fourth element."""
     B, Sq, H, D = q.shape
     Hkv = k.shape[2]
     if scale is None:
         scale = D ** -0.5
     ke = expand_kv(k, H)
     ve = expand_kv(v, H)
-    s = _scores(q, ke, causal, scale, dtype)
+    s = _scores(q, ke, causal, scale, dtype, bias)
     p = torch.exp(s - lse.to(dtype).unsqueeze(-1))  # (B, H, Sq, Sk)
     if causal:
         p = p.masked_fill(_causal_mask(Sq, ke.shape[1], p.device), 0.0)
@@ -158,7 +170,18 @@ def attention_backward(
         g = H // Hkv
         dk = dk.reshape(B, dk.shape[1], Hkv, g, D).sum(3)
         dv = dv.reshape(B, dv.shape[1], Hkv, g, D).sum(3)
-    return dq, dk.contiguous(), dv.contiguous()
+    if bias is None:
+        return dq, dk.contiguous(), dv.contiguous()
+    return dq, dk.contiguous(), dv.contiguous(), reduce_to_bias_shape(ds, bias.shape)
+
+
+def reduce_to_bias_shape(ds: torch.Tensor, shape) -> torch.Tensor:
+    """Sum a (B, H, Sq, Sk) score gradient over the dimensions a bias of
+    ``shape`` (B|1, H|1, Sq, Sk) broadcasts."""
+    for dim in (0, 1):
+        if shape[dim] == 1 and ds.shape[dim] != 1:
+            ds = ds.sum(dim, keepdim=True)
+    return ds.contiguous()
 
 
 def attention_autograd(
@@ -168,18 +191,23 @@ def attention_autograd(
     dropout_mask: Optional[torch.Tensor] = None,
     dropout_p: float = 0.0,
     dtype: torch.dtype = torch.float64,
+    bias: Optional[torch.Tensor] = None,
 ):
     """(O, LSE, dQ, dK, dV) with the gradients taken by torch.autograd through
-    :func:`attention_forward` (a second, independent route to the backward)."""
+    :func:`attention_forward` (a second, independent route to the backward);
+    with ``bias`` also dBias as a sixth element."""
     qq = q.detach().to(dtype).requires_grad_(True)
     kk = k.detach().to(dtype).requires_grad_(True)
     vv = v.detach().to(dtype).requires_grad_(True)
-    o, lse = attention_forward(qq, kk, vv, causal, scale, dropout_mask, dropout_p, dtype)
+    bb = None if bias is None else bias.detach().to(dtype).requires_grad_(True)
+    o, lse = attention_forward(qq, kk, vv, causal, scale, dropout_mask, dropout_p, dtype, bb)
     o.backward(do.to(dtype))
-    return o.detach(), lse.detach(), qq.grad, kk.grad, vv.grad
+    if bb is None:
+        return o.detach(), lse.detach(), qq.grad, kk.grad, vv.grad
+    return o.detach(), lse.detach(), qq.grad, kk.grad, vv.grad, bb.grad
 
 
-def brute_force_forward(q, k, v, causal=False, scale=None, keep=None, dropout_p=0.0):
+def brute_force_forward(q, k, v, causal=False, scale=None, keep=None, dropout_p=0.0, bias=None):
     """Scalar-loop forward in Python floats for tiny shapes: an implementation
     that shares no code with :func:`attention_forward` (used to pin it)."""
     B, Sq, H, D = q.shape
@@ -188,6 +216,7 @@ def brute_force_forward(q, k, v, causal=False, scale=None, keep=None, dropout_p=
     if scale is None:
         scale = D ** -0.5
     qf, kf, vf = q.double().tolist(), k.double().tolist(), v.double().tolist()
+    bf = None if bias is None else bias.double().tolist()
     o = [[[[0.0] * D for _ in range(H)] for _ in range(Sq)] for _ in range(B)]
     lse = [[[float("-inf")] * Sq for _ in range(H)] for _ in range(B)]
     for b in range(B):
@@ -198,6 +227,9 @@ def brute_force_forward(q, k, v, causal=False, scale=None, keep=None, dropout_p=
                 if not js:
                     continue
                 sc = {j: scale * sum(qf[b][i][h][d] * kf[b][j][hk][d] for d in range(D)) for j in js}
+                if bf is not None:
+                    bb, bh = (b if len(bf) > 1 else 0), (h if len(bf[0]) > 1 else 0)
+                    sc = {j: x + bf[bb][bh][i][j] for j, x in sc.items()}
                 m = max(sc.values())
                 tot = sum(math.exp(x - m) for x in sc.values())
                 lse[b][h][i] = m + math.log(tot)

@@ -235,6 +235,95 @@ def test_backward_invariants():
         assert torch.allclose(dv.sum(1), do.sum(1), atol=1e-12)
 
 
+# ----------------------------------------------------------------------------- additive bias
+
+BIAS_SHAPES = [(2, 3), (1, 3), (2, 1), (1, 1)]  # (B|1, H|1) with B = 2, H = 3
+
+
+@pytest.mark.parametrize("bshape", BIAS_SHAPES)
+@pytest.mark.parametrize("causal", [False, True])
+def test_bias_forward_vs_brute_force(bshape, causal):
+    B, Sq, Sk, H, Hkv, D = 2, 6, 5, 3, 3, 4
+    q, k, v = _rand((B, Sq, H, D), 111), _rand((B, Sk, Hkv, D), 112), _rand((B, Sk, Hkv, D), 113)
+    bias = _rand((*bshape, Sq, Sk), 114)
+    o, lse = oa.attention_forward(q, k, v, causal, 0.6, bias=bias)
+    ob, lb = oa.brute_force_forward(q, k, v, causal, 0.6, bias=bias)
+    assert torch.allclose(o, ob, atol=1e-12, rtol=0) and torch.allclose(lse, lb, atol=1e-12, rtol=0)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_bias_forward_vs_sdpa_float_mask(causal):
+    # SDPA adds a float attn_mask to the scaled scores: the same operation
+    B, S, H, D = 2, 17, 3, 8
+    q, k, v = _rand((B, S, H, D), 121), _rand((B, S, H, D), 122), _rand((B, S, H, D), 123)
+    bias = _rand((1, H, S, S), 124)
+    mask = bias.expand(B, H, S, S).clone()
+    if causal:
+        mask = mask.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool), 1), float("-inf"))
+    o, _ = oa.attention_forward(q, k, v, causal, 0.3, bias=bias)
+    ref = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                         attn_mask=mask, scale=0.3).transpose(1, 2)
+    assert torch.allclose(o, ref, atol=1e-12, rtol=0)
+
+
+def test_bias_closed_forms():
+    B, S, H, D = 1, 9, 2, 4
+    q, k, v = _rand((B, S, H, D), 131), _rand((B, S, H, D), 132), _rand((B, S, H, D), 133)
+    o0, l0 = oa.attention_forward(q, k, v, False)
+    # a bias constant along the keys shifts LSE and leaves O unchanged
+    row = _rand((1, H, S, 1), 134)
+    o1, l1 = oa.attention_forward(q, k, v, False, bias=row.expand(1, H, S, S))
+    assert torch.allclose(o1, o0, atol=1e-13) and torch.allclose(l1, l0 + row[..., 0], atol=1e-13)
+    # a -inf bias on key j is the same as removing key j
+    bias = torch.zeros(1, 1, S, S, dtype=torch.float64)
+    bias[..., 3] = float("-inf")
+    keep = [j for j in range(S) if j != 3]
+    o2, l2 = oa.attention_forward(q, k, v, False, bias=bias)
+    o3, l3 = oa.attention_forward(q, k[:, keep], v[:, keep], False)
+    assert torch.allclose(o2, o3, atol=1e-13) and torch.allclose(l2, l3, atol=1e-13)
+
+
+@pytest.mark.parametrize("bshape", BIAS_SHAPES)
+def test_bias_backward_formulas_vs_autograd(bshape):
+    B, Sq, Sk, H, Hkv, D = 2, 7, 6, 3, 3, 4
+    q, k, v = _rand((B, Sq, H, D), 141), _rand((B, Sk, Hkv, D), 142), _rand((B, Sk, Hkv, D), 143)
+    do = _rand((B, Sq, H, D), 144)
+    bias = _rand((*bshape, Sq, Sk), 145)
+    o, lse, dq, dk, dv, db = oa.attention_autograd(q, k, v, do, True, 0.5, bias=bias)
+    dq2, dk2, dv2, db2 = oa.attention_backward(q, k, v, o, do, lse, True, 0.5, bias=bias)
+    assert db.shape == bias.shape
+    for a, b in ((dq, dq2), (dk, dk2), (dv, dv2), (db, db2)):
+        assert torch.allclose(a, b, atol=1e-12, rtol=0)
+
+
+def test_bias_gradient_invariants():
+    # dBias = dS: its rows sum to zero (sum_j P_ij (dP_ij - delta_i) = 0), it is
+    # zero where the causal mask removes a key, and a broadcast bias gets the
+    # sum of the full-shape gradient over the broadcast dimensions
+    B, S, H, D = 2, 8, 3, 4
+    q, k, v, do = (_rand((B, S, H, D), s) for s in (151, 152, 153, 154))
+    full = _rand((B, H, S, S), 155)
+    *_, dfull = oa.attention_autograd(q, k, v, do, True, bias=full)
+    assert torch.allclose(dfull.sum(-1), torch.zeros_like(dfull.sum(-1)), atol=1e-12)
+    assert torch.equal(dfull.masked_select(torch.triu(torch.ones(S, S, dtype=torch.bool), 1).expand_as(dfull)),
+                       torch.zeros(B * H * S * (S - 1) // 2, dtype=torch.float64))
+    shared = full[:1, :1]
+    *_, dshared = oa.attention_autograd(q, k, v, do, True, bias=shared)
+    *_, dexp = oa.attention_autograd(q, k, v, do, True, bias=shared.expand(B, H, S, S).contiguous())
+    assert torch.allclose(dshared, dexp.sum((0, 1), keepdim=True), atol=1e-12)
+
+
+def test_planted_mistake_scaled_bias_is_caught(monkeypatch):
+    # bias added before the scale (scale * (qk + bias)) instead of after it
+    q, k, v = _rand((1, 5, 2, 4), 161), _rand((1, 5, 2, 4), 162), _rand((1, 5, 2, 4), 163)
+    bias = _rand((1, 2, 5, 5), 164)
+    ob, _ = oa.brute_force_forward(q, k, v, False, 0.5, bias=bias)
+    orig = oa._scores
+    monkeypatch.setattr(oa, "_scores", lambda q_, k_, c, s, d, b=None: orig(q_, k_, c, s, d, None if b is None else b * s))
+    o, _ = oa.attention_forward(q, k, v, False, 0.5, bias=bias)
+    assert not torch.allclose(o, ob, atol=1e-6)
+
+
 # ----------------------------------------------------------------------------- planted mistakes
 
 def test_planted_mistake_wrong_causal_diagonal_is_caught(monkeypatch):
@@ -250,7 +339,7 @@ def test_planted_mistake_dropped_scale_is_caught(monkeypatch):
     q, k, v = _rand((1, 5, 1, 4), 91), _rand((1, 5, 1, 4), 92), _rand((1, 5, 1, 4), 93)
     ob, lb = oa.brute_force_forward(q, k, v, False, 0.5)
     orig = oa._scores
-    monkeypatch.setattr(oa, "_scores", lambda q_, k_, c, s, d: orig(q_, k_, c, 1.0, d))
+    monkeypatch.setattr(oa, "_scores", lambda q_, k_, c, s, d, b=None: orig(q_, k_, c, 1.0, d, b))
     o, lse = oa.attention_forward(q, k, v, False, 0.5)
     assert not torch.allclose(lse, lb, atol=1e-6)
 
