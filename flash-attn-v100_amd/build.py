@@ -29,6 +29,11 @@ SOURCES = [
     "fa_kernels_bf16.hip",
     "fa_kernels_f16.hip",
     "fa_kernels_f32.hip",
+    "fa_bias_bf16.hip",
+    "fa_bias_f16.hip",
+    "fa_bias_f32.hip",
+    "fa_bias32_bf16.hip",
+    "fa_bias32_f16.hip",
 ]
 
 

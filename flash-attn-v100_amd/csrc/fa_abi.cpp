@@ -62,6 +62,30 @@ int32_t check_span(const int64_t st[4], int32_t S, int32_t D, int es) {
     return span < (1LL << 31) ? FA_OK : FA_ERR_TOO_LARGE;
 }
 
+// Optional bias: element type = the input dtype or float32; (b, h, i, j)
+// strides, j stride 1, the others non-negative multiples of 16 bytes (zero
+// broadcasts), base 16-byte aligned; the kernels read 4 consecutive keys of a
+// row with one 8- or 16-byte load.
+int32_t check_bias(const void* bias, const int64_t st[4], int32_t bias_dtype, int32_t dtype) {
+    if (!bias) return FA_OK;
+    if (bias_dtype != dtype && bias_dtype != FA_DTYPE_F32) return FA_ERR_BIAS;
+    const int es = elem_size(bias_dtype);
+    if (!aligned16(bias) || st[3] != 1) return FA_ERR_BIAS;
+    for (int i = 0; i < 3; ++i)
+        if (st[i] < 0 || (st[i] * es) % 16 != 0) return FA_ERR_BIAS;
+    return FA_OK;
+}
+
+// Optional bias gradient (float32): j stride 1, 4-byte aligned base,
+// non-negative strides (the kernels store one float per (query, key)).
+int32_t check_dbias(const float* dbias, const int64_t st[4]) {
+    if (!dbias) return FA_OK;
+    if (((uintptr_t)dbias & 3u) || st[3] != 1) return FA_ERR_BIAS;
+    for (int i = 0; i < 3; ++i)
+        if (st[i] < 0) return FA_ERR_BIAS;
+    return FA_OK;
+}
+
 // Backward workspace: B * H rows of 2 * sq_pad float32 (LSE * log2 e, then
 // delta), sq_pad = Sq rounded up to kSqPad; total rounded up to 256 bytes.
 size_t ws_bytes_for(const fa_bwd_args* a) {
@@ -91,6 +115,9 @@ const char* fa_strerror(int32_t code) {
         case FA_ERR_SCALE: return "scale must be finite and > 0";
         case FA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
         case FA_ERR_TOO_LARGE: return "problem too large for the kernel grid";
+        case FA_ERR_BIAS:
+            return "bias needs the input dtype or float32, j stride 1, b/h/i strides multiples of 16 bytes and a "
+                   "16-byte aligned base; dbias needs a bias, j stride 1 and a 4-byte aligned base";
         default: return "unknown status code";
     }
 }
@@ -115,7 +142,7 @@ int32_t fa_fwd_check(const fa_fwd_args* a) {
         (st = check_span(a->v_stride, a->seqlen_k, a->head_dim, es)) ||
         (st = check_span(a->o_stride, a->seqlen_q, a->head_dim, es)))
         return st;
-    return FA_OK;
+    return check_bias(a->bias, a->bias_stride, a->bias_dtype, a->dtype);
 }
 
 int32_t fa_fwd(const fa_fwd_args* a, void* stream) {
@@ -145,9 +172,25 @@ int32_t fa_fwd(const fa_fwd_args* a, void* stream) {
     p.rp = 1.f / (1.f - a->dropout_p);
     p.seed = a->seed;
     p.offset = a->offset;
+    p.bias = a->bias;
+    p.bias_sb = a->bias_stride[0];
+    p.bias_sh = a->bias_stride[1];
+    p.bias_ss = a->bias_stride[2];
     const bool causal = a->causal != 0;
     const bool dropout = a->dropout_p > 0.f;
     hipStream_t s = (hipStream_t)stream;
+    if (a->bias) {
+        const bool b32 = a->bias_dtype == FA_DTYPE_F32;
+        switch (a->dtype) {
+            case FA_DTYPE_BF16:
+                return status_of(b32 ? fa::launch_fwd_bias32_bf16(p, a->head_dim, causal, dropout, s)
+                                     : fa::launch_fwd_bias_bf16(p, a->head_dim, causal, dropout, s));
+            case FA_DTYPE_F16:
+                return status_of(b32 ? fa::launch_fwd_bias32_f16(p, a->head_dim, causal, dropout, s)
+                                     : fa::launch_fwd_bias_f16(p, a->head_dim, causal, dropout, s));
+            default: return status_of(fa::launch_fwd_bias_f32(p, a->head_dim, causal, dropout, s));
+        }
+    }
     switch (a->dtype) {
         case FA_DTYPE_BF16: return status_of(fa::launch_fwd_bf16(p, a->head_dim, causal, dropout, s));
         case FA_DTYPE_F16: return status_of(fa::launch_fwd_f16(p, a->head_dim, causal, dropout, s));
@@ -186,6 +229,10 @@ int32_t fa_bwd_check(const fa_bwd_args* a, size_t ws_bytes) {
                              a->seqlen_q, a->seqlen_q, a->seqlen_k, a->seqlen_k};
     for (int i = 0; i < 8; ++i)
         if ((st = check_span(strides[i], rows[i], a->head_dim, es))) return st;
+    if (a->dbias && !a->bias) return FA_ERR_BIAS;
+    if ((st = check_bias(a->bias, a->bias_stride, a->bias_dtype, a->dtype)) ||
+        (st = check_dbias(a->dbias, a->dbias_stride)))
+        return st;
     const size_t need = fa_bwd_workspace_size(a);
     if (need > 0 && ws_bytes < need) return FA_ERR_WORKSPACE;
     return FA_OK;
@@ -234,9 +281,30 @@ int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int
     p.rp = 1.f / (1.f - a->dropout_p);
     p.seed = a->seed;
     p.offset = a->offset;
+    p.bias = a->bias;
+    p.bias_sb = a->bias_stride[0];
+    p.bias_sh = a->bias_stride[1];
+    p.bias_ss = a->bias_stride[2];
+    p.dbias = a->dbias;
+    p.dbias_sb = a->dbias_stride[0];
+    p.dbias_sh = a->dbias_stride[1];
+    p.dbias_ss = a->dbias_stride[2];
     const bool causal = a->causal != 0;
     const bool dropout = a->dropout_p > 0.f;
     hipStream_t s = (hipStream_t)stream;
+    if (a->bias) {
+        const bool b32 = a->bias_dtype == FA_DTYPE_F32;
+        const int D = a->head_dim;
+        switch (a->dtype) {
+            case FA_DTYPE_BF16:
+                return status_of(b32 ? fa::launch_bwd_bias32_bf16(p, D, causal, dropout, stage, s)
+                                     : fa::launch_bwd_bias_bf16(p, D, causal, dropout, stage, s));
+            case FA_DTYPE_F16:
+                return status_of(b32 ? fa::launch_bwd_bias32_f16(p, D, causal, dropout, stage, s)
+                                     : fa::launch_bwd_bias_f16(p, D, causal, dropout, stage, s));
+            default: return status_of(fa::launch_bwd_bias_f32(p, D, causal, dropout, stage, s));
+        }
+    }
     switch (a->dtype) {
         case FA_DTYPE_BF16: return status_of(fa::launch_bwd_bf16(p, a->head_dim, causal, dropout, stage, s));
         case FA_DTYPE_F16: return status_of(fa::launch_bwd_f16(p, a->head_dim, causal, dropout, stage, s));

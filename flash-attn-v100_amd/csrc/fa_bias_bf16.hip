@@ -1,0 +1,17 @@
+// Forward and backward kernel instantiations for bf16 inputs (D in {32, 64, 128},
+// causal x dropout), with an additive bias of the input dtype.  One translation unit per dtype and bias mode
+// keeps builds parallel.
+#include "fa_bwd.hpp"
+#include "fa_fwd.hpp"
+
+namespace fa {
+
+hipError_t launch_fwd_bias_bf16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s) {
+    return launch_fwd_dispatch<bf16, bf16>(p, D, causal, dropout, s);
+}
+
+hipError_t launch_bwd_bias_bf16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s) {
+    return launch_bwd_dispatch<bf16, bf16>(p, D, causal, dropout, stage, s);
+}
+
+}  // namespace fa

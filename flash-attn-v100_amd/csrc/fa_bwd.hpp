@@ -18,6 +18,9 @@
 //      (double-buffered) and consumed as two 32-key sub-steps, K^T read from
 //      the K tile with transposing reads.
 // Diagonal (causal) tiles run a separate masking variant of each tile step.
+// With an additive bias (BIAS) both kernels add bias * log2 e to the scores
+// before the exponent; dkdv_kernel, the one kernel that visits every
+// (query, key) pair once, also writes dBias = dS (fp32, unscaled) when asked.
 // All five products accumulate in fp32 and are rounded once to the input dtype.
 #pragma once
 
@@ -100,9 +103,12 @@ struct DkdvCfg {
     static_assert(BUF_BYTES % 16 == 0, "16-byte aligned buffers");
 };
 
-template <typename T, int D, bool CAUSAL, bool DROPOUT>
+// TB: element type of the additive bias (T or float), void = no bias
+template <typename T, int D, bool CAUSAL, bool DROPOUT, typename TB>
 __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const int n_ktiles) {
     using C = DkdvCfg<T, D>;
+    constexpr bool BIAS = !std::is_void<TB>::value;
+    using BT = typename std::conditional<BIAS, TB, T>::type;
     constexpr int BQ = C::BQ, RW = C::RW;
     __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
 
@@ -208,6 +214,22 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
         }
     };
 
+    // ---- bias of this lane's key for the 16 queries {8 g + 4 hi + e} of a sub-step ----
+    constexpr int NBI = BIAS ? 16 : 1;
+    bias1_t<BT> braw[NBI];
+    const int kjc = min(kj, p.Sk - 1);  // keys past Sk are clamped into range (never stored)
+    auto load_bias = [&](int it, int st) FA_INLINE {
+        if constexpr (BIAS) {
+            const BT* bcol = (const BT*)p.bias + b * p.bias_sb + tile_head(it) * p.bias_sh + kjc;
+            const int qb0 = tile_q0(it) + 32 * st;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int q = min(qb0 + 8 * (r >> 2) + 4 * hi + (r & 3), p.Sq - 1);
+                braw[r] = load_bias1(bcol + (int64_t)q * p.bias_ss);
+            }
+        }
+    };
+
     // ---- P and dS of tile `it` (buffer s); dS = P (dP - delta), scale applied at the end ----
     constexpr int NPK = C::F32 ? 1 : 2;
     float pd[16], ds[16];
@@ -217,6 +239,8 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
         const float* lse2 = (const float*)(buf(s) + 2 * C::QALLOC) + 32 * st;
         const float* dels = lse2 + BQ;
         const int qb0 = tile_q0(it) + 32 * st;
+        float* dbcol = nullptr;
+        if (BIAS && p.dbias) dbcol = p.dbias + b * p.dbias_sb + tile_head(it) * p.dbias_sh + kj;
         uint64_t col_ctr = 0;
         if (DROPOUT)
             col_ctr = p.offset + (uint64_t)(b * p.H + tile_head(it)) * (uint64_t)p.Sq * (uint64_t)p.Sk + (uint64_t)kj;
@@ -228,7 +252,11 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
             for (int e = 0; e < 4; ++e) {
                 const int r = 4 * g + e;
                 const int q = qb0 + 8 * g + 4 * hi + e;
-                float pv = fast_exp2(__builtin_fmaf(sc[r], c, -l4[e]));
+                float pv;
+                if constexpr (BIAS)
+                    pv = fast_exp2(__builtin_fmaf(sc[r], c, bias_log2<BT>(braw[r]) - l4[e]));
+                else
+                    pv = fast_exp2(__builtin_fmaf(sc[r], c, -l4[e]));
                 if (MASK && q < kj) pv = 0.f;
                 float dpv = dpc[r];
                 float pdv = pv;
@@ -240,6 +268,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
                 }
                 pd[r] = pdv;
                 ds[r] = pv * (dpv - d4[e]);
+                if (BIAS && dbcol && q < p.Sq && kj < p.Sk) dbcol[(int64_t)q * p.dbias_ss] = ds[r];
             }
         }
         if constexpr (!C::F32) {
@@ -300,6 +329,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
         issue(min(it + 1, total - 1), bcur ^ 1);
 #pragma unroll
         for (int st = 0; st < C::NSUB; ++st) {
+            load_bias(it, st);
             sdp(bcur, st, sc, dpc);
             softmax_ds(it, bcur, st, sc, dpc, mask_tag);
             dkdv_acc(bcur, st, I0{});
@@ -381,9 +411,11 @@ struct DqCfg {
     static constexpr int MIN_BLOCKS = (F32 && D == 128) ? 1 : 2;
 };
 
-template <typename T, int D, bool CAUSAL, bool DROPOUT>
+template <typename T, int D, bool CAUSAL, bool DROPOUT, typename TB>
 __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(const BwdParams p, const int n_qtiles) {
     using C = DqCfg<T, D>;
+    constexpr bool BIAS = !std::is_void<TB>::value;
+    using BT = typename std::conditional<BIAS, TB, T>::type;
     constexpr int BN = C::BN, KW = C::KW;
     __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
 
@@ -456,12 +488,24 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
     int bcur = 0;
     if (n_tiles > 0) issue(0, 0);
 
+    // bias of this lane's query row (rows past Sq clamped into range, never stored)
+    const BT* brow = nullptr;
+    if constexpr (BIAS)
+        brow = (const BT*)p.bias + b * p.bias_sb + h * p.bias_sh + (int64_t)min(qi, p.Sq - 1) * p.bias_ss;
+
     // one 32-key sub-step of the tile in buffer `bcur` starting at key k0
     auto sub = [&](int k0, const T* Ks, const T* Vs, auto mask_tag) FA_INLINE {
         constexpr bool MASK = decltype(mask_tag)::value;
         constexpr int BN = 32;
         const bool active = !MASK || !CAUSAL || k0 <= qw0 + 31;
         if (active) {
+            // bias of keys {8 g + 4 hi + 0..3}
+            bias4_t<BT> bv[BIAS ? 4 : 1];
+            if constexpr (BIAS) {
+                const bool full = k0 + BN <= p.Sk;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) bv[g] = load_bias4(brow, k0 + 8 * g + 4 * hi, p.Sk, full);
+            }
             // ---- S^T = K Q^T, dP^T = V dO^T (C[key][query]) ----
             f32x16 s = f32x16{}, dp = f32x16{};
             const T* krow = Ks + l32 * KW;
@@ -493,7 +537,11 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = k0 + 8 * (r >> 2) + 4 * hi + (r & 3);
-                float pv = fast_exp2(__builtin_fmaf(s[r], c, -lse2));
+                float pv;
+                if constexpr (BIAS)
+                    pv = fast_exp2(__builtin_fmaf(s[r], c, bias_log2<BT>(bv[r >> 2][r & 3]) - lse2));
+                else
+                    pv = fast_exp2(__builtin_fmaf(s[r], c, -lse2));
                 if (need_mask && (key >= p.Sk || (CAUSAL && key > qi))) pv = 0.f;
                 float dpv = dp[r];
                 if (DROPOUT) {
@@ -581,7 +629,7 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
 }
 
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool CAUSAL, bool DROPOUT>
+template <typename T, int D, bool CAUSAL, bool DROPOUT, typename TB>
 hipError_t launch_bwd_t(const BwdParams& p, int stage, hipStream_t s) {
     if (stage < 0 || stage == 0) {
         constexpr int EPC = 16 / sizeof(T);
@@ -594,25 +642,25 @@ hipError_t launch_bwd_t(const BwdParams& p, int stage, hipStream_t s) {
         using C = DkdvCfg<T, D>;
         const int nk = (p.Sk + C::BK - 1) / C::BK;
         const int64_t nb = (int64_t)nk * p.Hkv * p.B;
-        if (nb > 0) hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, DROPOUT>), dim3((unsigned)nb), dim3(C::NT), 0, s, p, nk);
+        if (nb > 0) hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, DROPOUT, TB>), dim3((unsigned)nb), dim3(C::NT), 0, s, p, nk);
     }
     if (stage < 0 || stage == 2) {
         using C = DqCfg<T, D>;
         const int nq = (p.Sq + C::BM - 1) / C::BM;
         const int64_t nb = (int64_t)nq * p.H * p.B;
-        if (nb > 0) hipLaunchKernelGGL((dq_kernel<T, D, CAUSAL, DROPOUT>), dim3((unsigned)nb), dim3(C::NT), 0, s, p, nq);
+        if (nb > 0) hipLaunchKernelGGL((dq_kernel<T, D, CAUSAL, DROPOUT, TB>), dim3((unsigned)nb), dim3(C::NT), 0, s, p, nq);
     }
     return hipGetLastError();
 }
 
-template <typename T>
+template <typename T, typename TB>
 hipError_t launch_bwd_dispatch(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s) {
 #define FA_BWD_CASE(DD)                                                                  \
     if (D == DD) {                                                                       \
-        if (causal) return dropout ? launch_bwd_t<T, DD, true, true>(p, stage, s)               \
-                                   : launch_bwd_t<T, DD, true, false>(p, stage, s);             \
-        return dropout ? launch_bwd_t<T, DD, false, true>(p, stage, s)                          \
-                       : launch_bwd_t<T, DD, false, false>(p, stage, s);                        \
+        if (causal) return dropout ? launch_bwd_t<T, DD, true, true, TB>(p, stage, s)  \
+                                   : launch_bwd_t<T, DD, true, false, TB>(p, stage, s); \
+        return dropout ? launch_bwd_t<T, DD, false, true, TB>(p, stage, s)             \
+                       : launch_bwd_t<T, DD, false, false, TB>(p, stage, s);           \
     }
     FA_BWD_CASE(32)
     FA_BWD_CASE(64)

@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 // Device helpers and kernel-local lambdas are always inlined: an out-of-line
 // call would keep tile descriptors and MFMA accumulators in scratch memory
 // (and turn wave-uniform buffer descriptors into per-lane ones).
@@ -97,6 +99,46 @@ __device__ FA_INLINE inline float pair_sum(float x) {
 }
 
 __device__ FA_INLINE inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------------------
+// additive bias (element type T, key stride 1)
+// Four consecutive keys of one bias row in raw form (one 8- or 16-byte load).
+template <typename T>
+using bias4_t = typename std::conditional<Elem<T>::kF32, f32x4, s16x4>::type;
+
+// keys key .. key+3 of `row`; when !full, keys >= Sk read as 0 (their scores
+// are masked) and are not touched
+template <typename T>
+__device__ FA_INLINE inline bias4_t<T> load_bias4(const T* row, int key, int Sk, bool full) {
+    using V = bias4_t<T>;
+    if (full) return *reinterpret_cast<const V*>(row + key);
+    V v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if constexpr (Elem<T>::kF32)
+            v[e] = key + e < Sk ? row[key + e] : 0.f;
+        else
+            v[e] = key + e < Sk ? __builtin_bit_cast(short, row[key + e]) : (short)0;
+    }
+    return v;
+}
+
+// raw bias element -> bias * log2(e)
+template <typename T>
+__device__ FA_INLINE inline float bias_log2(float x) { return x * kLog2e; }
+template <typename T>
+__device__ FA_INLINE inline float bias_log2(short x) { return Elem<T>::unpack1(x) * kLog2e; }
+
+// one raw bias element (16-bit types as short)
+template <typename T>
+using bias1_t = typename std::conditional<Elem<T>::kF32, float, short>::type;
+template <typename T>
+__device__ FA_INLINE inline bias1_t<T> load_bias1(const T* p) {
+    if constexpr (Elem<T>::kF32)
+        return *p;
+    else
+        return __builtin_bit_cast(short, *p);
+}
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also fences global
 // memory, which on gfx9 (one counter for vector loads and stores) makes every

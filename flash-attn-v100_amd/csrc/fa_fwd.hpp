@@ -20,6 +20,10 @@
 //     wave's last query are skipped by that wave; only diagonal and tail tiles
 //     run the masking variant of the tile step.
 //   * fp32 inputs use v_mfma_f32_32x32x2_f32 with fp32 P.
+//   * optional additive bias (BIAS): each lane reads 4 consecutive keys of its
+//     query's bias row per load, issued with the tile's S MFMAs; the scores
+//     then become t = S * scale * log2 e + bias * log2 e (one FMA) before the
+//     mask, and the softmax runs on t (reference forward_kernel.py:166-182).
 #pragma once
 
 #include <type_traits>
@@ -48,9 +52,12 @@ struct FwdCfg {
     static_assert(NW * 32 * OW <= SMEM_ELEMS, "O staging must fit in the K/V buffers");
 };
 
-template <typename T, int D, bool CAUSAL, bool DROPOUT>
+// TB: element type of the additive bias (T or float), void = no bias
+template <typename T, int D, bool CAUSAL, bool DROPOUT, typename TB>
 __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     using C = FwdCfg<T, D>;
+    constexpr bool BIAS = !std::is_void<TB>::value;
+    using BT = typename std::conditional<BIAS, TB, T>::type;
     constexpr int BN = C::BN, NB = C::NB, KW = C::KW, VW = C::VW;
     __shared__ __attribute__((aligned(16))) T smem[C::SMEM_ELEMS];
 
@@ -97,7 +104,33 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     float m_run = -1e30f;  // running max in log2 units (scores * scale * log2 e)
     float l_run = 0.f;     // lane-partial row sum of exp2(t - m_run)
     float m_raw = -INFINITY;
-    const float c = p.scale_log2;
+    // score -> log2 units; with a bias the scores are converted (and the bias
+    // added) before the max, so the softmax factor is 1
+    const float c = BIAS ? 1.f : p.scale_log2;
+
+    // ---- bias: 4-key groups {32 blk + 8 g + 4 hi + 0..3} of this lane's row ----
+    constexpr int NG = BIAS ? NB * 4 : 1;
+    bias4_t<BT> bv[NG];
+    const BT* brow = nullptr;
+    if constexpr (BIAS)  // rows past Sq are clamped into range (never stored)
+        brow = (const BT*)p.bias + b * p.bias_sb + h * p.bias_sh + (int64_t)min(qi, p.Sq - 1) * p.bias_ss;
+    auto load_bias = [&](int k0) FA_INLINE {
+        if constexpr (BIAS) {
+            const bool full = k0 + BN <= p.Sk;
+#pragma unroll
+            for (int g = 0; g < NG; ++g) bv[g] = load_bias4(brow, k0 + 32 * (g >> 2) + 8 * (g & 3) + 4 * hi, p.Sk, full);
+        }
+    };
+    // t = S * scale * log2 e + bias * log2 e
+    auto add_bias = [&](f32x16 (&s)[NB]) FA_INLINE {
+        if constexpr (BIAS) {
+#pragma unroll
+            for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    s[blk][r] = __builtin_fmaf(s[blk][r], p.scale_log2, bias_log2<BT>(bv[4 * blk + (r >> 2)][r & 3]));
+        }
+    };
 
     uint64_t row_ctr = 0;
     if (DROPOUT) row_ctr = p.offset + ((uint64_t)(b * p.H + h) * (uint64_t)p.Sq + (uint64_t)qi) * (uint64_t)p.Sk;
@@ -267,7 +300,9 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     }
     sync_tiles();
     if (n_w > 0) {
+        load_bias(0);
         qk(Ks0, sa);
+        add_bias(sa);
         if (n_plain == 0) mask(sa, 0);
         update_max(sa);
     }
@@ -280,11 +315,15 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
         const bool act = !MASK || j < n_w;
         const bool next = !MASK || j + 1 < n_w;
         if (act) {
-            if (next) qk(Ks0 + ((j + 1) & 1) * C::KTILE, sn);
+            if (next) {
+                load_bias((j + 1) * BN);
+                qk(Ks0 + ((j + 1) & 1) * C::KTILE, sn);
+            }
             softmax(sc, pk, j * BN);
         }
         if (act) pv(Vs0 + (j & 1) * C::VTILE, sc, pk);
         if (act && next) {
+            add_bias(sn);
             if (MASK) mask(sn, (j + 1) * BN);
             update_max(sn);
         }
@@ -316,7 +355,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     if (hi == 0 && qi < p.Sq) {
         const int64_t si = (int64_t)(b * p.H + h) * p.Sq + qi;
         p.lse[si] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
-        if (p.mx) p.mx[si] = m_raw * p.scale;
+        if (p.mx) p.mx[si] = m_raw * (BIAS ? kLn2 : p.scale);
     }
     sync_tiles();  // all waves done with the K/V buffers and no copy still in flight
     constexpr int OW = C::OW;
@@ -353,25 +392,25 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     }
 }
 
-template <typename T, int D, bool CAUSAL, bool DROPOUT>
+template <typename T, int D, bool CAUSAL, bool DROPOUT, typename TB>
 hipError_t launch_fwd_t(const FwdParams& p, hipStream_t s) {
     using C = FwdCfg<T, D>;
     FwdParams q = p;
     q.n_qtiles = (p.Sq + C::BM - 1) / C::BM;
     const int64_t nblocks = (int64_t)q.n_qtiles * p.H * p.B;
     if (nblocks <= 0) return hipSuccess;
-    hipLaunchKernelGGL((fwd_kernel<T, D, CAUSAL, DROPOUT>), dim3((unsigned)nblocks), dim3(C::NT), 0, s, q);
+    hipLaunchKernelGGL((fwd_kernel<T, D, CAUSAL, DROPOUT, TB>), dim3((unsigned)nblocks), dim3(C::NT), 0, s, q);
     return hipGetLastError();
 }
 
-template <typename T>
+template <typename T, typename TB>
 hipError_t launch_fwd_dispatch(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s) {
 #define FA_FWD_CASE(DD)                                                                  \
     if (D == DD) {                                                                       \
-        if (causal) return dropout ? launch_fwd_t<T, DD, true, true>(p, s)               \
-                                   : launch_fwd_t<T, DD, true, false>(p, s);             \
-        return dropout ? launch_fwd_t<T, DD, false, true>(p, s)                          \
-                       : launch_fwd_t<T, DD, false, false>(p, s);                        \
+        if (causal) return dropout ? launch_fwd_t<T, DD, true, true, TB>(p, s)         \
+                                   : launch_fwd_t<T, DD, true, false, TB>(p, s);       \
+        return dropout ? launch_fwd_t<T, DD, false, true, TB>(p, s)                    \
+                       : launch_fwd_t<T, DD, false, false, TB>(p, s);                  \
     }
     FA_FWD_CASE(32)
     FA_FWD_CASE(64)

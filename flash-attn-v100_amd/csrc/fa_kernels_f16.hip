@@ -1,16 +1,17 @@
 // Forward and backward kernel instantiations for f16 inputs (D in {32, 64, 128},
-// causal x dropout).  One translation unit per dtype keeps builds parallel.
+// causal x dropout), without a bias.  One translation unit per dtype and bias mode
+// keeps builds parallel.
 #include "fa_bwd.hpp"
 #include "fa_fwd.hpp"
 
 namespace fa {
 
 hipError_t launch_fwd_f16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s) {
-    return launch_fwd_dispatch<f16>(p, D, causal, dropout, s);
+    return launch_fwd_dispatch<f16, void>(p, D, causal, dropout, s);
 }
 
 hipError_t launch_bwd_f16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s) {
-    return launch_bwd_dispatch<f16>(p, D, causal, dropout, stage, s);
+    return launch_bwd_dispatch<f16, void>(p, D, causal, dropout, stage, s);
 }
 
 }  // namespace fa

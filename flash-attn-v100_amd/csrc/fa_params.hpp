@@ -26,6 +26,10 @@ struct FwdParams {
     float dropout_p;
     float rp;          // 1 / (1 - dropout_p)
     uint64_t seed, offset;
+    // optional additive bias (B, H, Sq, Sk) in the input dtype or float32; a
+    // zero stride broadcasts that dimension, the key stride is 1
+    const void* bias;
+    int64_t bias_sb, bias_sh, bias_ss;
 };
 
 struct BwdParams {
@@ -55,20 +59,36 @@ struct BwdParams {
     int ws_stride;  // 2 * sq_pad
     float scale, scale_log2, dropout_p, rp;
     uint64_t seed, offset;
+    const void* bias;  // as in FwdParams
+    int64_t bias_sb, bias_sh, bias_ss;
+    float* dbias;      // optional fp32 (B, H, Sq, Sk) gradient of the bias, key stride 1
+    int64_t dbias_sb, dbias_sh, dbias_ss;
 };
 
 // per-(batch, head) rows of the backward workspace are padded to a multiple
 // of this many queries, so query tiles read whole rows without range checks
 constexpr int kSqPad = 128;
 
-// dtype-specific launchers (fa_kernels_{bf16,f16,f32}.hip)
+// dtype-specific launchers: fa_kernels_{bf16,f16,f32}.hip without a bias,
+// fa_bias_{bf16,f16,f32}.hip with a bias of the input dtype,
+// fa_bias32_{bf16,f16}.hip with a float32 bias
 hipError_t launch_fwd_bf16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
 hipError_t launch_fwd_f16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
 hipError_t launch_fwd_f32(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
+hipError_t launch_fwd_bias_bf16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
+hipError_t launch_fwd_bias_f16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
+hipError_t launch_fwd_bias_f32(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
+hipError_t launch_fwd_bias32_bf16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
+hipError_t launch_fwd_bias32_f16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
 // stage: 0 = delta pre-pass, 1 = dK/dV, 2 = dQ, -1 = all three in order
 hipError_t launch_bwd_bf16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
 hipError_t launch_bwd_f16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
 hipError_t launch_bwd_f32(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
+hipError_t launch_bwd_bias_bf16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
+hipError_t launch_bwd_bias_f16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
+hipError_t launch_bwd_bias_f32(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
+hipError_t launch_bwd_bias32_bf16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
+hipError_t launch_bwd_bias32_f16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
 // fa_misc.hip
 hipError_t launch_dropout_mask(uint64_t seed, uint64_t offset, int B, int H, int Sq, int Sk, float p,
                                uint8_t* keep, hipStream_t s);

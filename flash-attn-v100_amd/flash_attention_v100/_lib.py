@@ -18,7 +18,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfa_gfx950.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 HEAD_DIMS = (32, 64, 128)
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
@@ -48,6 +48,7 @@ class FwdArgs(ctypes.Structure):
         ("dtype", ctypes.c_int32), ("causal", ctypes.c_int32),
         ("scale", ctypes.c_float), ("dropout_p", ctypes.c_float),
         ("seed", ctypes.c_uint64), ("offset", ctypes.c_uint64),
+        ("bias", ctypes.c_void_p), ("bias_stride", _I64x4), ("bias_dtype", ctypes.c_int32),
     ]
 
 
@@ -63,6 +64,8 @@ class BwdArgs(ctypes.Structure):
         ("dtype", ctypes.c_int32), ("causal", ctypes.c_int32),
         ("scale", ctypes.c_float), ("dropout_p", ctypes.c_float),
         ("seed", ctypes.c_uint64), ("offset", ctypes.c_uint64),
+        ("bias", ctypes.c_void_p), ("bias_stride", _I64x4), ("bias_dtype", ctypes.c_int32),
+        ("dbias", ctypes.c_void_p), ("dbias_stride", _I64x4),
     ]
 
 
@@ -155,31 +158,96 @@ def seed_offset(seed: Optional[int], offset: Optional[int]) -> Tuple[int, int]:
     return int(seed) & 0xFFFFFFFFFFFFFFFF, int(offset) & 0xFFFFFFFFFFFFFFFF
 
 
-def fwd_args(q, k, v, o, lse, max_vals, causal, scale, dropout_p, seed, offset) -> FwdArgs:
+class PreparedBias:
+    """An additive bias in the layout the kernels read: ``tensor`` viewed as
+    (B, H, Sq, Sk) with zero strides on broadcast dimensions, key stride 1,
+    other strides multiples of 16 bytes, 16-byte aligned base; element type the
+    input dtype or float32.  ``shape`` and ``dtype`` are the caller's, for the
+    gradient."""
+
+    __slots__ = ("tensor", "strides", "dtype_code", "shape", "dtype")
+
+    def __init__(self, tensor, strides, dtype_code, shape, dtype):
+        self.tensor, self.strides, self.dtype_code, self.shape, self.dtype = tensor, strides, dtype_code, shape, dtype
+
+
+def prepare_bias(bias: torch.Tensor, B: int, H: int, Sq: int, Sk: int, dtype: torch.dtype) -> PreparedBias:
+    """Validate a (B|1, H|1, Sq|1, Sk) bias (the reference's shapes,
+    ops/attention.py:58 and forward_kernel.py:166-182, plus a broadcast query
+    dimension) and bring it into the kernels' layout.  A bias in the input dtype
+    or float32 is read as it is; any other dtype is converted to float32 (exact
+    for float16/bfloat16), so the bias is added in fp32 as the reference's Triton
+    kernel did.  Rows are copied into a 16-byte padded buffer only when the
+    given strides or base do not meet the kernels' alignment."""
+    if not isinstance(bias, torch.Tensor) or bias.dim() != 4:
+        raise ValueError("bias must be a 4-D tensor [batch|1, heads|1, seq_len_q|1, seq_len_k]")
+    shape = tuple(bias.shape)
+    want = (B, H, Sq, Sk)
+    for d in range(4):
+        if shape[d] not in (1, want[d]):
+            raise ValueError(f"bias shape {shape} is not broadcastable to {want}")
+    orig_dtype = bias.dtype
+    t = bias if bias.dtype in (dtype, torch.float32) else bias.to(torch.float32)
+    if shape[3] != Sk:  # keys must be contiguous: materialise a broadcast key dimension
+        t = t.expand(*shape[:3], Sk)
+    es = t.element_size()
+    strides = [0 if t.shape[d] == 1 else t.stride(d) for d in range(3)] + [1]
+    ok = (t.stride(3) == 1 or Sk <= 1) and t.data_ptr() % 16 == 0 and all(
+        s >= 0 and (s * es) % 16 == 0 for s in strides[:3])
+    if not ok:
+        pad = -(-max(Sk, 1) * es // 16) * 16 // es
+        buf = torch.zeros((t.shape[0], t.shape[1], t.shape[2], pad), device=t.device, dtype=t.dtype)
+        buf[..., :Sk] = t
+        t = buf
+        strides = [0 if t.shape[d] == 1 else t.stride(d) for d in range(3)] + [1]
+    return PreparedBias(t, _I64x4(*strides), DTYPE_CODES[t.dtype], shape, orig_dtype)
+
+
+def reduce_dbias(dbias: torch.Tensor, pb: PreparedBias) -> torch.Tensor:
+    """Sum the (B, H, Sq, Sk) float32 score gradient over the dimensions the
+    caller's bias broadcast and cast it to the bias's dtype."""
+    dims = [d for d in range(4) if pb.shape[d] == 1 and dbias.shape[d] != 1]
+    g = dbias.sum(dim=dims, keepdim=True) if dims else dbias
+    return g.to(pb.dtype)
+
+
+def fwd_args(q, k, v, o, lse, max_vals, causal, scale, dropout_p, seed, offset, bias=None) -> FwdArgs:
     B, Sq, H, D = q.shape
     return FwdArgs(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
         max_vals.data_ptr() if max_vals is not None else None,
         _strides(q), _strides(k), _strides(v), _strides(o),
         B, Sq, k.shape[1], H, k.shape[2], D, DTYPE_CODES[q.dtype], int(bool(causal)),
-        float(scale), float(dropout_p), seed, offset)
+        float(scale), float(dropout_p), seed, offset,
+        bias.tensor.data_ptr() if bias is not None else None,
+        bias.strides if bias is not None else _I64x4(0, 0, 0, 1),
+        bias.dtype_code if bias is not None else DTYPE_CODES[q.dtype])
+
+
+def _as_prepared(bias, q, k) -> Optional[PreparedBias]:
+    if bias is None or isinstance(bias, PreparedBias):
+        return bias
+    return prepare_bias(bias, q.shape[0], q.shape[2], q.shape[1], k.shape[1], q.dtype)
 
 
 def fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: float,
-        dropout_p: float = 0.0, seed: int = 0, offset: int = 0, want_max: bool = False):
-    """Run ``fa_fwd``: returns (o, lse, max_vals or None).  Inputs (B, S, H, D)."""
+        dropout_p: float = 0.0, seed: int = 0, offset: int = 0, want_max: bool = False, bias=None):
+    """Run ``fa_fwd``: returns (o, lse, max_vals or None).  Inputs (B, S, H, D);
+    ``bias`` a (B|1, H|1, Sq|1, Sk) tensor or a :class:`PreparedBias`."""
     lib = load()
     q, k, v = prepare(q), prepare(k), prepare(v)
+    pb = _as_prepared(bias, q, k)
     B, Sq, H, _ = q.shape
     o = torch.empty_like(q, memory_format=torch.contiguous_format)
     lse = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32)
     mx = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32) if want_max else None
-    a = fwd_args(q, k, v, o, lse, mx, causal, scale, dropout_p, seed, offset)
+    a = fwd_args(q, k, v, o, lse, mx, causal, scale, dropout_p, seed, offset, pb)
     _check("fa_fwd", lib.fa_fwd(ctypes.byref(a), _stream(q)))
     return o, lse, mx
 
 
-def bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, offset) -> BwdArgs:
+def bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, offset,
+             bias=None, dbias=None) -> BwdArgs:
     B, Sq, H, D = q.shape
     return BwdArgs(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(),
@@ -187,22 +255,39 @@ def bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, of
         _strides(q), _strides(k), _strides(v), _strides(o), _strides(do),
         _strides(dq), _strides(dk), _strides(dv),
         B, Sq, k.shape[1], H, k.shape[2], D, DTYPE_CODES[q.dtype], int(bool(causal)),
-        float(scale), float(dropout_p), seed, offset)
+        float(scale), float(dropout_p), seed, offset,
+        bias.tensor.data_ptr() if bias is not None else None,
+        bias.strides if bias is not None else _I64x4(0, 0, 0, 1),
+        bias.dtype_code if bias is not None else DTYPE_CODES[q.dtype],
+        dbias.data_ptr() if dbias is not None else None,
+        _strides(dbias) if dbias is not None else _I64x4(0, 0, 0, 1))
 
 
 def bwd(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float = 0.0,
-        seed: int = 0, offset: int = 0):
-    """Run ``fa_bwd``: returns (dq, dk, dv) in the input dtype."""
+        seed: int = 0, offset: int = 0, bias=None, want_dbias: bool = False):
+    """Run ``fa_bwd``: returns (dq, dk, dv) in the input dtype, plus the bias
+    gradient in the caller's bias shape and dtype when ``want_dbias``."""
     lib = load()
     q, k, v, o, do = (prepare(t) for t in (q, k, v, o, do))
+    pb = _as_prepared(bias, q, k)
+    if want_dbias and pb is None:
+        raise ValueError("want_dbias needs a bias")
     lse = lse.contiguous()
     dq = torch.empty_like(q, memory_format=torch.contiguous_format)
     dk = torch.empty_like(k, memory_format=torch.contiguous_format)
     dv = torch.empty_like(v, memory_format=torch.contiguous_format)
-    a = bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, offset)
+    dbias = None
+    if want_dbias:
+        B, Sq, H, _ = q.shape
+        # causal: (query, key) pairs of tiles the kernels skip keep their zero
+        alloc = torch.zeros if causal else torch.empty
+        dbias = alloc((B, H, Sq, k.shape[1]), device=q.device, dtype=torch.float32)
+    a = bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, offset, pb, dbias)
     ws_bytes = lib.fa_bwd_workspace_size(ctypes.byref(a))
     ws = torch.empty(max(int(ws_bytes), 256), device=q.device, dtype=torch.uint8)
     _check("fa_bwd", lib.fa_bwd(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(q)))
+    if want_dbias:
+        return dq, dk, dv, reduce_dbias(dbias, pb)
     return dq, dk, dv
 
 

@@ -12,7 +12,7 @@ reference's ``utils.py:227-254`` scans cost a sync each).
 
 Fallback (reference ``interface.py:331-348, 453-490``): with
 ``fallback_on_error=True`` a request the gfx950 kernels do not implement
-(``NotImplementedError``: additive bias, an uncompiled head_dim) or reject as a
+(``NotImplementedError``: an uncompiled head_dim) or reject as a
 tile hint (``ValueError`` from ``block_size_m/n``) is served by PyTorch math on
 the same GPU, with a warning.  Everything else raises: a missing kernel library
 (:class:`FlashAttentionExtensionError`), a kernel error, CPU tensors (there is
@@ -70,9 +70,12 @@ def validate_inputs_enhanced(q, k, v, scale=None, bias=None, dropout_p=0.0):
         raise ValueError("Flash Attention requires GPU tensors (there is no CPU path)")
     if bias is not None:
         if not isinstance(bias, torch.Tensor) or bias.dim() != 4:
-            raise ValueError("bias must be a 4-D tensor [batch|1, heads|1, seq_len_q, seq_len_k]")
-        if bias.shape[-2:] != (Sq, Sk) or bias.shape[0] not in (1, B) or bias.shape[1] not in (1, Hq):
+            raise ValueError("bias must be a 4-D tensor [batch|1, heads|1, seq_len_q|1, seq_len_k]")
+        if (bias.shape[3] != Sk or bias.shape[2] not in (1, Sq) or bias.shape[0] not in (1, B)
+                or bias.shape[1] not in (1, Hq)):
             raise ValueError(f"bias shape {tuple(bias.shape)} is not broadcastable to {(B, Hq, Sq, Sk)}")
+        if bias.device != q.device:
+            raise ValueError(f"bias must be on {q.device}, got {bias.device}")
     if not (0.0 <= dropout_p < 1.0):
         raise ValueError(f"dropout_p must be in [0.0, 1.0), got {dropout_p}")
     if scale is None:

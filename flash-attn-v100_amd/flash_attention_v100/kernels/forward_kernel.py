@@ -5,8 +5,10 @@
 ``flash_attention_forward_autotuned_enhanced`` (``:445-512``) both return
 ``(o, lse, max_vals)``: ``o`` in the input dtype, ``lse`` and ``max_vals``
 (B, H, Sq) float32.  Here ``lse`` is the natural-log logsumexp of the scaled,
-masked scores (the reference stored the row sum under that name) and
-``max_vals`` the row max of the scaled scores.  The Triton-tuning switches
+biased, masked scores (the reference stored the row sum under that name) and
+``max_vals`` the row max of the scaled, biased scores.  ``bias`` is an additive
+(B|1, H|1, Sq|1, Sk) tensor added in fp32 after the scale and before the causal
+mask, as at ``kernels/forward_kernel.py:166-182``.  The Triton-tuning switches
 (warp specialisation, double buffering, prefetch, fast math) are accepted and
 have no effect: the gfx950 kernel always double-buffers K/V and uses exp2.
 """
@@ -17,7 +19,7 @@ from typing import Optional, Tuple
 import torch
 
 from .. import _lib
-from ..ops.attention import _check_kernel_inputs, check_block_sizes
+from ..ops.attention import _check_kernel_inputs, _prepare_bias, check_block_sizes
 
 
 def flash_attention_forward_triton_enhanced(
@@ -37,12 +39,11 @@ def flash_attention_forward_triton_enhanced(
     dropout_seed: Optional[int] = None,
     dropout_offset: Optional[int] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    if bias is not None:
-        raise NotImplementedError("additive attention bias is not supported by the gfx950 kernels")
     check_block_sizes(block_size_m, block_size_n)
     _check_kernel_inputs(q, k, v, dropout_p)
+    pb = _prepare_bias(bias, q, k)
     seed, offset = _lib.seed_offset(dropout_seed, dropout_offset) if dropout_p > 0 else (0, 0)
-    return _lib.fwd(q, k, v, causal, scale, dropout_p, seed, offset, want_max=True)
+    return _lib.fwd(q, k, v, causal, scale, dropout_p, seed, offset, want_max=True, bias=pb)
 
 
 def flash_attention_forward_autotuned_enhanced(

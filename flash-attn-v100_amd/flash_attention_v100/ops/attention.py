@@ -9,9 +9,14 @@ when ``return_softmax_lse`` and one gradient slot per input in ``backward``
 offset so the backward regenerates the forward's mask (the reference never saved
 them, ``:209-227``).
 
+An additive ``bias`` of shape (B|1, H|1, Sq|1, Sk) is added to the scaled
+scores inside the kernels (reference ``kernels/forward_kernel.py:166-182``)
+and, when the bias requires grad, its real gradient dS (summed over broadcast
+dimensions) is returned in the bias slot; the reference returned zeros there
+(``ops/attention.py:297-301``).
+
 Deliberate differences, each raising instead of silently computing something
-else: ``bias`` and multi-GPU execution are not implemented by these kernels
-(``NotImplementedError``; the public ``flash_attention_v100`` can fall back);
+else: multi-GPU execution is out of scope (``NotImplementedError``);
 ``enable_gradient_checkpointing`` is accepted and has nothing to do (the
 backward already recomputes P tile by tile); ``block_size_m/n`` are validated
 hints, the gfx950 tile shape is fixed per (dtype, head_dim).
@@ -54,6 +59,14 @@ def _check_kernel_inputs(q, k, v, dropout_p):
         raise ValueError(f"dropout_p must be in [0.0, 1.0), got {dropout_p}")
 
 
+def _prepare_bias(bias, q, k):
+    if bias is None:
+        return None
+    if not isinstance(bias, torch.Tensor) or bias.device != q.device:
+        raise ValueError("bias must be a tensor on the same device as q")
+    return _lib.prepare_bias(bias, q.shape[0], q.shape[2], q.shape[1], k.shape[1], q.dtype)
+
+
 class EnhancedFlashAttentionV100Function(torch.autograd.Function):
     """FlashAttention forward/backward on the gfx950 HIP kernels."""
 
@@ -82,17 +95,20 @@ class EnhancedFlashAttentionV100Function(torch.autograd.Function):
         dropout_seed: Optional[int] = None,
         dropout_offset: Optional[int] = None,
     ):
-        if bias is not None:
-            raise NotImplementedError("additive attention bias is not supported by the gfx950 kernels")
         if enable_multi_gpu and world_size > 1:
             raise NotImplementedError("multi-GPU execution is out of scope for this single-GPU build")
         check_block_sizes(block_size_m, block_size_n)
         _check_kernel_inputs(q, k, v, dropout_p)
         if scale is None:
             scale = q.shape[-1] ** -0.5
+        pb = _prepare_bias(bias, q, k)
         seed, offset = _lib.seed_offset(dropout_seed, dropout_offset) if dropout_p > 0 else (0, 0)
-        o, lse, _ = _lib.fwd(q, k, v, causal, scale, dropout_p, seed, offset)
-        ctx.save_for_backward(q, k, v, o, lse)
+        o, lse, _ = _lib.fwd(q, k, v, causal, scale, dropout_p, seed, offset, bias=pb)
+        if pb is None:
+            ctx.save_for_backward(q, k, v, o, lse)
+        else:
+            ctx.save_for_backward(q, k, v, o, lse, pb.tensor)
+        ctx.bias_meta = None if pb is None else (pb.strides, pb.dtype_code, pb.shape, pb.dtype)
         ctx.scale = scale
         ctx.causal = causal
         ctx.dropout_p = dropout_p
@@ -109,14 +125,20 @@ class EnhancedFlashAttentionV100Function(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_output: torch.Tensor, grad_softmax_lse: Optional[torch.Tensor] = None):
         # grad_softmax_lse is ignored, as in the reference (ops/attention.py:234-333)
-        q, k, v, o, lse = ctx.saved_tensors
-        dq, dk, dv = _lib.bwd(q, k, v, o, grad_output, lse, ctx.causal, ctx.scale,
-                              ctx.dropout_p, ctx.seed, ctx.offset)
+        saved = ctx.saved_tensors
+        q, k, v, o, lse = saved[:5]
+        pb = None if ctx.bias_meta is None else _lib.PreparedBias(saved[5], *ctx.bias_meta)
+        want_dbias = pb is not None and ctx.needs_input_grad[6]
+        grads = _lib.bwd(q, k, v, o, grad_output, lse, ctx.causal, ctx.scale,
+                         ctx.dropout_p, ctx.seed, ctx.offset, bias=pb, want_dbias=want_dbias)
+        dq, dk, dv = grads[:3]
         return (
             dq if ctx.needs_input_grad[0] else None,
             dk if ctx.needs_input_grad[1] else None,
             dv if ctx.needs_input_grad[2] else None,
-            None, None, None, None, None, None, None, None, None, None,
+            None, None, None,
+            grads[3] if want_dbias else None,
+            None, None, None, None, None, None,
             None, None, None, None, None, None, None, None,
         )
 

@@ -12,6 +12,14 @@
  * lse / max_vals are (B, H, Sq) float32, contiguous.
  * Query head h reads KV head h / (H / Hkv).  Causal masks key j > query i
  * (top-left aligned, also when Sq != Sk).
+ *
+ * Optional additive bias (NULL = none), logically (B, H, Sq, Sk), element type
+ * bias_dtype (the input dtype or FA_DTYPE_F32), strides in ELEMENTS in the
+ * order (b, h, i, j): a stride of 0 broadcasts that dimension (the reference's
+ * (B|1, H|1, Sq, Sk) shapes); the j stride must be 1, the b/h/i strides
+ * multiples of 16 bytes, and the base 16-byte aligned.  It is added in fp32 to
+ * the scaled scores before the causal mask (reference
+ * forward_kernel.py:166-182).
  */
 #ifndef FA_ABI_H
 #define FA_ABI_H
@@ -23,7 +31,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 1
+#define FA_ABI_VERSION 2
 
 /* element types */
 #define FA_DTYPE_F16 0
@@ -46,6 +54,7 @@ extern "C" {
 #define FA_ERR_TOO_LARGE -12  /* a grid dimension would overflow, or max(S, 256) rows
                                  of one (batch, head) slice of a tensor span >= 2^31
                                  bytes (S = its sequence length) */
+#define FA_ERR_BIAS -13       /* bias / dbias dtype, strides or alignment violate the rules above */
 
 /* Forward arguments.
  * Replaces the launcher flash_attention_forward_triton_enhanced
@@ -80,6 +89,9 @@ typedef struct fa_fwd_args {
     float dropout_p;
     uint64_t seed;
     uint64_t offset;
+    const void* bias;        /* optional additive bias (NULL = none), see the file comment */
+    int64_t bias_stride[4];  /* (b, h, i, j) in elements */
+    int32_t bias_dtype;      /* dtype, or FA_DTYPE_F32 */
 } fa_fwd_args;
 
 /* Backward arguments.
@@ -88,7 +100,12 @@ typedef struct fa_fwd_args {
  * FlashAttentionV100Function.backward at ops/attention.py:288-294.  It reads
  * the saved (q, k, v, o, lse) plus the dropout seed/offset of the forward
  * (the reference dropped them, ops/attention.py:209-227) and writes dq, dk,
- * dv in the input dtype (fully overwritten, no zero-init needed). */
+ * dv in the input dtype (fully overwritten, no zero-init needed).  With a
+ * bias, the forward's bias is passed again; if dbias is non-NULL the kernels
+ * also write dS = d loss / d(scaled score + bias) into it, float32, logically
+ * (B, H, Sq, Sk) with its own (b, h, i, j) strides (no broadcast: a caller
+ * with a broadcast bias sums over those dimensions; the reference returned
+ * zeros, ops/attention.py:297-301). */
 typedef struct fa_bwd_args {
     const void* q;
     const void* k;
@@ -119,6 +136,11 @@ typedef struct fa_bwd_args {
     float dropout_p;
     uint64_t seed;
     uint64_t offset;
+    const void* bias;         /* optional, as in fa_fwd_args */
+    int64_t bias_stride[4];
+    int32_t bias_dtype;
+    float* dbias;             /* optional float32 (B, H, Sq, Sk) gradient of the bias */
+    int64_t dbias_stride[4];  /* (b, h, i, j) in elements; j stride 1, i stride a multiple of 4 */
 } fa_bwd_args;
 
 /* Library ABI version (FA_ABI_VERSION).  No reference counterpart. */

@@ -25,7 +25,7 @@ is the textbook math, with
   ``tests/test_attention.py:63``), also when Sq != Sk;
 * grouped KV heads: query head ``h`` reads KV head ``h // (H // Hkv)``
   (``utils.py:88-97`` allows ``H % Hkv == 0``);
-* an optional additive bias of shape (B|1, H|1, Sq, Sk) is added to the scaled
+* an optional additive bias of shape (B|1, H|1, Sq|1, Sk) is added to the scaled
   scores before the causal mask (``forward_kernel.py:166-182``: ``qk * scale``,
   ``+ bias_block``, then ``tl.where(causal_mask, qk, -inf)``).
 
@@ -101,7 +101,7 @@ def attention_forward(
     """Forward O (B, Sq, H, D) in ``dtype`` and LSE (B, H, Sq) in ``dtype``.
 
     ``dropout_mask`` is a bool keep-mask (B, H, Sq, Sk) or None; ``bias`` an
-    additive (B|1, H|1, Sq, Sk) tensor or None.
+    additive (B|1, H|1, Sq|1, Sk) tensor or None.
     Rows with no unmasked key (only possible when Sk == 0) give O = 0 and
     LSE = -inf.
     """
@@ -177,8 +177,8 @@ def attention_backward(
 
 def reduce_to_bias_shape(ds: torch.Tensor, shape) -> torch.Tensor:
     """Sum a (B, H, Sq, Sk) score gradient over the dimensions a bias of
-    ``shape`` (B|1, H|1, Sq, Sk) broadcasts."""
-    for dim in (0, 1):
+    ``shape`` (B|1, H|1, Sq|1, Sk) broadcasts."""
+    for dim in (0, 1, 2):
         if shape[dim] == 1 and ds.shape[dim] != 1:
             ds = ds.sum(dim, keepdim=True)
     return ds.contiguous()
@@ -229,7 +229,8 @@ def brute_force_forward(q, k, v, causal=False, scale=None, keep=None, dropout_p=
                 sc = {j: scale * sum(qf[b][i][h][d] * kf[b][j][hk][d] for d in range(D)) for j in js}
                 if bf is not None:
                     bb, bh = (b if len(bf) > 1 else 0), (h if len(bf[0]) > 1 else 0)
-                    sc = {j: x + bf[bb][bh][i][j] for j, x in sc.items()}
+                    bi = i if len(bf[bb][bh]) > 1 else 0
+                    sc = {j: x + bf[bb][bh][bi][j] for j, x in sc.items()}
                 m = max(sc.values())
                 tot = sum(math.exp(x - m) for x in sc.values())
                 lse[b][h][i] = m + math.log(tot)

@@ -55,10 +55,12 @@ def make_inputs(B, Sq, H, D, dtype, Sk=None, Hkv=None, seed=42, qk_scale=1.0, de
     return tuple(t.to(dtype).to(device) for t in (q, k, v, do))
 
 
-def lowp_math(q, k, v, do, causal, scale, keep=None, p=0.0, with_bwd=True):
+def lowp_math(q, k, v, do, causal, scale, keep=None, p=0.0, with_bwd=True, bias=None):
     """The reference's math path (tests/test_attention.py:39-79) evaluated in
     the inputs' dtype (the error envelope), with explicit backward formulas.
-    dK/dV come back per query head (see reduce_kv).
+    dK/dV come back per query head (see reduce_kv).  With an additive ``bias``
+    (added in the inputs' dtype after the scale) dBias = dS, summed in float32
+    over the broadcast dimensions and rounded to the bias's dtype, is appended.
     Every matmul operand is made contiguous (bf16 batched products with
     transposed views are avoided)."""
     dt = q.dtype
@@ -69,6 +71,8 @@ def lowp_math(q, k, v, do, causal, scale, keep=None, p=0.0, with_bwd=True):
     kh = k.transpose(1, 2).contiguous()
     vh = v.transpose(1, 2).contiguous()
     s = torch.matmul(qh, kh.transpose(-2, -1).contiguous()) * scale
+    if bias is not None:
+        s = s + bias.to(dt)
     if causal:
         m = torch.triu(torch.ones(s.shape[-2], s.shape[-1], dtype=torch.bool, device=s.device), diagonal=1)
         s = s.masked_fill(m, float("-inf"))
@@ -91,6 +95,9 @@ def lowp_math(q, k, v, do, causal, scale, keep=None, p=0.0, with_bwd=True):
     dq = torch.matmul(ds, kh) * scale
     dk = dk.transpose(1, 2)
     dv = dv.transpose(1, 2)
+    if bias is not None:
+        db = oa.reduce_to_bias_shape(ds.float(), bias.shape).to(bias.dtype)
+        return o.transpose(1, 2), lse, dq.transpose(1, 2), dk, dv, db
     return o.transpose(1, 2), lse, dq.transpose(1, 2), dk, dv
 
 

@@ -26,7 +26,7 @@ def declared_functions():
 
 def test_library_loads_and_version():
     lib = _lib.load()
-    assert lib.fa_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.fa_abi_version() == _lib.ABI_VERSION == 2
 
 
 def test_exports_every_declared_function():
@@ -58,10 +58,12 @@ int main(void) {
   printf("fa_bwd_args sizeof %zu\n", sizeof(fa_bwd_args));
   F(fa_fwd_args, q) F(fa_fwd_args, max_vals) F(fa_fwd_args, q_stride) F(fa_fwd_args, o_stride)
   F(fa_fwd_args, batch) F(fa_fwd_args, causal) F(fa_fwd_args, scale) F(fa_fwd_args, dropout_p)
-  F(fa_fwd_args, seed) F(fa_fwd_args, offset)
+  F(fa_fwd_args, seed) F(fa_fwd_args, offset) F(fa_fwd_args, bias) F(fa_fwd_args, bias_stride)
+  F(fa_fwd_args, bias_dtype)
   F(fa_bwd_args, dout) F(fa_bwd_args, lse) F(fa_bwd_args, dv) F(fa_bwd_args, do_stride)
   F(fa_bwd_args, dv_stride) F(fa_bwd_args, batch) F(fa_bwd_args, causal) F(fa_bwd_args, scale)
-  F(fa_bwd_args, seed) F(fa_bwd_args, offset)
+  F(fa_bwd_args, seed) F(fa_bwd_args, offset) F(fa_bwd_args, bias) F(fa_bwd_args, bias_stride)
+  F(fa_bwd_args, bias_dtype) F(fa_bwd_args, dbias) F(fa_bwd_args, dbias_stride)
   return 0;
 }
 """
@@ -192,3 +194,84 @@ def test_rng_hooks_validation():
     assert lib.fa_rand(1, None, -1, None, None) == CODES["FA_ERR_SHAPE"]
     assert lib.fa_rand(1, None, 0, None, None) == CODES["FA_OK"]
     assert lib.fa_rand(1, None, 5, None, None) == CODES["FA_ERR_NULL_ARG"]
+
+
+# ----------------------------------------------------------------------------- bias
+
+def _cpu_bias_fwd(bias_shape=(2, 4, 64, 64), dtype=torch.float16, bias_dtype=None):
+    a, keep = _cpu_fwd(dtype=dtype)
+    bias = torch.zeros(bias_shape, dtype=bias_dtype or dtype)
+    pb = _lib.prepare_bias(bias, 2, 4, 64, 64, dtype)
+    a.bias = pb.tensor.data_ptr()
+    a.bias_stride = pb.strides
+    a.bias_dtype = pb.dtype_code
+    return a, (keep, pb)
+
+
+@pytest.mark.parametrize("shape", [(2, 4, 64, 64), (1, 4, 64, 64), (2, 1, 64, 64), (1, 1, 64, 64), (1, 1, 1, 64)])
+def test_bias_check_accepts_broadcast_shapes(shape):
+    for dt, bdt in ((torch.float16, None), (torch.bfloat16, torch.float32), (torch.float32, None)):
+        a, _keep = _cpu_bias_fwd(shape, dt, bdt)
+        assert _status(a) == CODES["FA_OK"], (shape, dt, bdt)
+
+
+def test_bias_check_rejects():
+    a, _keep = _cpu_bias_fwd()
+    a.bias_dtype = 1  # bf16 bias with fp16 inputs
+    assert _status(a) == CODES["FA_ERR_BIAS"]
+    a, _keep = _cpu_bias_fwd()
+    a.bias_stride[3] = 2
+    assert _status(a) == CODES["FA_ERR_BIAS"]
+    a, _keep = _cpu_bias_fwd()
+    a.bias_stride[2] = 65  # row stride not a multiple of 16 bytes
+    assert _status(a) == CODES["FA_ERR_BIAS"]
+    a, _keep = _cpu_bias_fwd()
+    a.bias = a.bias + 8
+    assert _status(a) == CODES["FA_ERR_BIAS"]
+
+
+def test_bwd_check_dbias_rules():
+    lib = _lib.load()
+    B, S, H, D = 2, 100, 3, 64
+    q = torch.zeros(B, S, H, D, dtype=torch.bfloat16)
+    lse = torch.zeros(B, H, S)
+    pb = _lib.prepare_bias(torch.zeros(1, H, S, S, dtype=torch.float32), B, H, S, S, q.dtype)
+    db = torch.zeros(B, H, S, S)
+    a = _lib.bwd_args(q, q, q, q, q, lse, q, q, q, True, 0.125, 0.0, 0, 0, pb, db)
+    ws = lib.fa_bwd_workspace_size(ctypes.byref(a))
+    assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_OK"]
+    a.dbias_stride[3] = 0
+    assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_ERR_BIAS"]
+    a = _lib.bwd_args(q, q, q, q, q, lse, q, q, q, True, 0.125, 0.0, 0, 0, None, db)
+    assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_ERR_BIAS"]  # dbias without a bias
+
+
+def test_prepare_bias_layout():
+    # unaligned rows (Sk = 13 halves = 26 bytes) are copied into 16-byte padded rows
+    b = torch.randn(2, 1, 5, 13).to(torch.float16)
+    pb = _lib.prepare_bias(b, 2, 3, 5, 13, torch.float16)
+    st = list(pb.strides)
+    assert st[1] == 0 and st[3] == 1 and (st[2] * 2) % 16 == 0 and (st[0] * 2) % 16 == 0
+    assert pb.tensor.data_ptr() % 16 == 0
+    assert torch.equal(pb.tensor[:, :, :, :13], b)
+    assert pb.shape == (2, 1, 5, 13) and pb.dtype == torch.float16
+    # aligned input: used in place
+    b2 = torch.randn(1, 3, 5, 16, dtype=torch.float32)
+    pb2 = _lib.prepare_bias(b2, 2, 3, 5, 16, torch.bfloat16)
+    assert pb2.tensor.data_ptr() == b2.data_ptr() and list(pb2.strides) == [0, 80, 16, 1]
+    assert pb2.dtype_code == _lib.DTYPE_CODES[torch.float32]
+    # other dtypes are widened to float32; bad shapes raise
+    pb3 = _lib.prepare_bias(torch.zeros(1, 1, 5, 16, dtype=torch.float64), 2, 3, 5, 16, torch.float16)
+    assert pb3.tensor.dtype == torch.float32
+    with pytest.raises(ValueError):
+        _lib.prepare_bias(torch.zeros(2, 2, 5, 16), 2, 3, 5, 16, torch.float16)
+    with pytest.raises(ValueError):
+        _lib.prepare_bias(torch.zeros(5, 16), 2, 3, 5, 16, torch.float16)
+
+
+def test_reduce_dbias_sums_broadcast_dims():
+    g = torch.arange(2 * 3 * 4 * 5, dtype=torch.float32).reshape(2, 3, 4, 5)
+    pb = _lib.PreparedBias(None, None, 2, (1, 3, 1, 5), torch.bfloat16)
+    r = _lib.reduce_dbias(g, pb)
+    assert r.shape == (1, 3, 1, 5) and r.dtype == torch.bfloat16
+    assert torch.equal(r.float(), g.sum(dim=(0, 2), keepdim=True).to(torch.bfloat16).float())

@@ -1,0 +1,201 @@
+"""Additive attention bias on the gfx950 kernels (through the C ABI and the
+autograd wrapper) against the float64 oracle: O, LSE, dQ, dK, dV and dBias.
+
+The bias is added to the scaled scores before the causal mask (reference
+kernels/forward_kernel.py:166-182); dBias = dS summed over the broadcast
+dimensions (the reference returned zeros, ops/attention.py:297-301).
+Tolerance as for the other parity tests: fp16/bf16 within 2x the error of the
+reference math run in the inputs' dtype (bias included) against the oracle;
+fp32 within 1e-5 of max|oracle|.
+"""
+import pytest
+import torch
+
+import flash_attention_v100 as fa
+from flash_attention_v100 import _lib
+from helpers import assert_parity, c_keep_mask, lowp_math, make_inputs, maxabs, reduce_kv
+from oracle import attention as oa
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+NAMES = ("O", "LSE", "dQ", "dK", "dV", "dBias")
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def make_bias(shape, dtype, seed=7, mag=2.0):
+    g = torch.Generator("cpu").manual_seed(seed)
+    return (torch.randn(shape, generator=g, dtype=torch.float32) * mag).to(dtype)
+
+
+def run_kernels(q, k, v, do, causal, scale, bias, p=0.0, seed=0, offset=0):
+    dev = [t.to(DEV) for t in (q, k, v, do)]
+    b = bias.to(DEV)
+    o, lse, _ = _lib.fwd(dev[0], dev[1], dev[2], causal, scale, p, seed, offset, bias=b)
+    dq, dk, dv, db = _lib.bwd(dev[0], dev[1], dev[2], o, dev[3], lse, causal, scale, p, seed, offset,
+                              bias=b, want_dbias=True)
+    torch.cuda.synchronize()
+    return o, lse, dq, dk, dv, db
+
+
+def check(q, k, v, do, causal, scale, bias, outs, keep=None, p=0.0, label=""):
+    """Whole-problem comparison (small shapes): float64 oracle on the CPU, the
+    envelope (lowp math in the inputs' dtype) on the GPU."""
+    o, lse = oa.attention_forward(q, k, v, causal, scale, keep, p, torch.float64, bias=bias)
+    refs = [o, lse] + list(oa.attention_backward(q, k, v, o, do, lse, causal, scale, keep, p, bias=bias))
+    res = {}
+    env = None
+    if q.dtype != torch.float32:
+        dev = [t.to(DEV) for t in (q, k, v, do)]
+        env = list(lowp_math(*dev, causal, scale, keep.to(DEV) if keep is not None else None, p,
+                             bias=bias.to(DEV)))
+        env[3] = reduce_kv(env[3], k.shape[2])
+        env[4] = reduce_kv(env[4], k.shape[2])
+    for i, n in enumerate(NAMES):
+        rf = refs[i]
+        ek = maxabs(outs[i].cpu(), rf)
+        ee = maxabs(env[i].cpu(), rf) if env is not None else None
+        res[n] = [ek, ee, rf.abs().max().item()]
+    assert_parity(res, q.dtype, label)
+    return res
+
+
+CASES = []
+for dt in (torch.float16, torch.bfloat16, torch.float32):
+    for D in (32, 64, 128):
+        for causal in (False, True):
+            CASES.append((dt, 2, 200, 200, 3, 3, D, causal, (2, 3, 200, 200), None))
+CASES += [
+    # broadcast shapes of the reference's (B|1, H|1, Sq, Sk), plus a key-padding row
+    (torch.bfloat16, 2, 160, 160, 4, 4, 64, True, (1, 4, 160, 160), None),
+    (torch.bfloat16, 2, 160, 160, 4, 4, 64, False, (2, 1, 160, 160), None),
+    (torch.float16, 2, 160, 160, 4, 4, 128, True, (1, 1, 160, 160), None),
+    (torch.float16, 2, 160, 160, 4, 4, 64, False, (2, 1, 1, 160), None),
+    # float32 bias with 16-bit inputs
+    (torch.bfloat16, 1, 150, 150, 4, 4, 128, True, (1, 4, 150, 150), torch.float32),
+    (torch.float16, 2, 100, 100, 2, 2, 64, False, (2, 2, 100, 100), torch.float32),
+    # ragged and unaligned rows (Sk * 2 bytes not a multiple of 16: padded copy), Sq != Sk
+    (torch.bfloat16, 1, 130, 77, 2, 2, 64, True, (1, 2, 130, 77), None),
+    (torch.float16, 1, 77, 261, 2, 2, 128, False, (1, 1, 77, 261), None),
+    (torch.float32, 1, 99, 13, 2, 2, 32, True, (1, 2, 99, 13), None),
+    # grouped KV heads
+    (torch.bfloat16, 2, 160, 160, 4, 2, 128, True, (2, 4, 160, 160), None),
+    (torch.float16, 1, 96, 96, 8, 1, 64, False, (1, 8, 96, 96), None),
+    # single query / key
+    (torch.bfloat16, 1, 1, 1, 2, 2, 64, True, (1, 2, 1, 1), None),
+    (torch.float16, 3, 1, 50, 2, 2, 32, False, (3, 2, 1, 50), None),
+]
+
+
+def _id(c):
+    dt, B, Sq, Sk, H, Hkv, D, causal, bshape, bdt = c
+    tag = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float32: "f32"}
+    return (f"{tag[dt]}-B{B}-Sq{Sq}-Sk{Sk}-H{H}-Hkv{Hkv}-D{D}-{'causal' if causal else 'full'}"
+            f"-bias{'x'.join(map(str, bshape))}{'-' + tag[bdt] if bdt else ''}")
+
+
+@pytest.mark.parametrize("case", CASES, ids=[_id(c) for c in CASES])
+def test_bias_fwd_bwd(case):
+    dt, B, Sq, Sk, H, Hkv, D, causal, bshape, bdt = case
+    say(f"case: bias {_id(case)}")
+    q, k, v, do = make_inputs(B, Sq, H, D, dt, Sk=Sk, Hkv=Hkv, seed=11)
+    bias = make_bias(bshape, bdt or dt)
+    scale = D ** -0.5
+    outs = run_kernels(q, k, v, do, causal, scale, bias)
+    assert outs[5].shape == bias.shape and outs[5].dtype == bias.dtype
+    check(q, k, v, do, causal, scale, bias, outs, label=_id(case))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_bias_with_dropout(causal):
+    B, S, H, D, p, seed, offset = 2, 180, 2, 64, 0.1, 1234, 77
+    say(f"case: bias + dropout causal={causal}")
+    q, k, v, do = make_inputs(B, S, H, D, torch.float32, seed=12)
+    bias = make_bias((1, H, S, S), torch.float32)
+    keep = torch.from_numpy(c_keep_mask(seed, offset, B, H, S, S, p)).bool()
+    outs = run_kernels(q, k, v, do, causal, D ** -0.5, bias, p, seed, offset)
+    check(q, k, v, do, causal, D ** -0.5, bias, outs, keep=keep, p=p, label="bias+dropout")
+
+
+def test_bias_minus_inf_key_padding():
+    # -inf entries remove keys (every row keeps some): same as dropping those keys
+    B, S, H, D = 2, 200, 2, 64
+    say("case: -inf key padding bias")
+    q, k, v, do = make_inputs(B, S, H, D, torch.float16, seed=13)
+    bias = torch.zeros(B, 1, 1, S, dtype=torch.float16)
+    bias[0, ..., 150:] = float("-inf")
+    bias[1, ..., 7::3] = float("-inf")
+    outs = run_kernels(q, k, v, do, False, D ** -0.5, bias)
+    for t in outs[:5]:
+        assert torch.isfinite(t).all()
+    check(q, k, v, do, False, D ** -0.5, bias, outs, label="-inf padding")
+    # batch 0 equals attention over its first 150 keys
+    o0, l0, _ = _lib.fwd(q[:1].to(DEV), k[:1, :150].to(DEV), v[:1, :150].to(DEV), False, D ** -0.5)
+    assert maxabs(outs[0][:1], o0) < 2e-3 and maxabs(outs[1][:1], l0) < 1e-3
+
+
+def test_float32_bias_keeps_precision_with_bf16_inputs():
+    # ALiBi-style bias with magnitudes in the hundreds: rounding it to bf16
+    # moves logits by up to 0.5, reading it as float32 does not
+    B, S, H, D = 1, 300, 2, 64
+    say("case: float32 ALiBi bias, bf16 inputs")
+    q, k, v, do = make_inputs(B, S, H, D, torch.bfloat16, seed=14)
+    i = torch.arange(S, dtype=torch.float32)
+    slopes = torch.tensor([0.5, 0.75]).view(1, H, 1, 1)
+    bias = -(slopes * (i.view(S, 1) - i.view(1, S)).abs()) + 100.0
+    ref, _ = oa.attention_forward(q, k, v, True, D ** -0.5, bias=bias)
+    o32, _, _ = _lib.fwd(q.to(DEV), k.to(DEV), v.to(DEV), True, D ** -0.5, bias=bias.to(DEV))
+    o16, _, _ = _lib.fwd(q.to(DEV), k.to(DEV), v.to(DEV), True, D ** -0.5, bias=bias.to(torch.bfloat16).to(DEV))
+    e32, e16 = maxabs(o32.cpu(), ref), maxabs(o16.cpu(), ref)
+    say(f"err fp32 bias {e32:.3e}  bf16-rounded bias {e16:.3e}")
+    assert e32 * 10 < e16
+
+
+def test_bias_max_vals_and_launchers():
+    B, S, H, D = 1, 256, 2, 64
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, S, H, D, torch.bfloat16, seed=15))
+    bias = make_bias((1, H, S, S), torch.bfloat16).to(DEV)
+    o, lse, mx = fa.flash_attention_forward_triton_enhanced(q, k, v, 0.125, True, bias=bias)
+    s = torch.matmul(q.float().transpose(1, 2), k.float().transpose(1, 2).transpose(-2, -1).contiguous()) * 0.125
+    s = s + bias.float()
+    s = s.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool, device=DEV), 1), float("-inf"))
+    assert torch.allclose(mx, s.amax(-1), atol=1e-3)
+    assert torch.allclose(lse, torch.logsumexp(s, -1), atol=1e-3)
+    dq, dk, dv, db = fa.flash_attention_backward_triton_enhanced(q, k, v, o, do, lse, mx, 0.125, True,
+                                                                 bias=bias, return_dbias=True)
+    dq2, dk2, dv2, db2 = _lib.bwd(q, k, v, o, do, lse, True, 0.125, bias=bias, want_dbias=True)
+    assert torch.equal(dq, dq2) and torch.equal(dk, dk2) and torch.equal(dv, dv2) and torch.equal(db, db2)
+
+
+def test_bias_grad_through_interface():
+    B, S, H, D = 2, 192, 4, 64
+    say("case: bias grad via flash_attention_v100")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, S, H, D, torch.float16, seed=16))
+    bias = make_bias((1, H, S, S), torch.float16).to(DEV)
+    qq, kk, vv, bb = (t.clone().requires_grad_(True) for t in (q, k, v, bias))
+    import warnings
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")  # no fallback warning: the kernels ran
+        o = fa.flash_attention_v100(qq, kk, vv, causal=True, bias=bb)
+    o.backward(do)
+    o2, lse2, _ = _lib.fwd(q, k, v, True, D ** -0.5, bias=bias)
+    dq, dk, dv, db = _lib.bwd(q, k, v, o2, do, lse2, True, D ** -0.5, bias=bias, want_dbias=True)
+    assert torch.equal(o, o2) and torch.equal(qq.grad, dq) and torch.equal(kk.grad, dk)
+    assert torch.equal(vv.grad, dv) and torch.equal(bb.grad, db)
+    # a bias without requires_grad gets no gradient and the same dQ/dK/dV
+    qq2 = q.clone().requires_grad_(True)
+    fa.flash_attention_v100(qq2, k, v, causal=True, bias=bias).backward(do)
+    assert torch.equal(qq2.grad, dq)
+    outs = (o2.cpu(), lse2.cpu(), dq.cpu(), dk.cpu(), dv.cpu(), db.cpu())
+    check(*(t.cpu() for t in (q, k, v, do)), True, D ** -0.5, bias.cpu(), outs, label="interface bias")
+
+
+def test_bias_deterministic():
+    q, k, v, do = (t.to(DEV) for t in make_inputs(1, 333, 4, 128, torch.bfloat16, seed=17))
+    bias = make_bias((1, 4, 333, 333), torch.bfloat16).to(DEV)
+    a = run_kernels(q, k, v, do, True, 0.1, bias)
+    b = run_kernels(q, k, v, do, True, 0.1, bias)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)

@@ -237,7 +237,13 @@ def test_backward_invariants():
 
 # ----------------------------------------------------------------------------- additive bias
 
-BIAS_SHAPES = [(2, 3), (1, 3), (2, 1), (1, 1)]  # (B|1, H|1) with B = 2, H = 3
+# (B|1, H|1, Sq|1) with B = 2, H = 3; None = the full query dimension
+BIAS_SHAPES = [(2, 3, None), (1, 3, None), (2, 1, None), (1, 1, None), (2, 1, 1)]
+
+
+def _bias_shape(bshape, Sq, Sk):
+    b, h, s = bshape
+    return (b, h, Sq if s is None else s, Sk)
 
 
 @pytest.mark.parametrize("bshape", BIAS_SHAPES)
@@ -245,7 +251,7 @@ BIAS_SHAPES = [(2, 3), (1, 3), (2, 1), (1, 1)]  # (B|1, H|1) with B = 2, H = 3
 def test_bias_forward_vs_brute_force(bshape, causal):
     B, Sq, Sk, H, Hkv, D = 2, 6, 5, 3, 3, 4
     q, k, v = _rand((B, Sq, H, D), 111), _rand((B, Sk, Hkv, D), 112), _rand((B, Sk, Hkv, D), 113)
-    bias = _rand((*bshape, Sq, Sk), 114)
+    bias = _rand(_bias_shape(bshape, Sq, Sk), 114)
     o, lse = oa.attention_forward(q, k, v, causal, 0.6, bias=bias)
     ob, lb = oa.brute_force_forward(q, k, v, causal, 0.6, bias=bias)
     assert torch.allclose(o, ob, atol=1e-12, rtol=0) and torch.allclose(lse, lb, atol=1e-12, rtol=0)
@@ -288,7 +294,7 @@ def test_bias_backward_formulas_vs_autograd(bshape):
     B, Sq, Sk, H, Hkv, D = 2, 7, 6, 3, 3, 4
     q, k, v = _rand((B, Sq, H, D), 141), _rand((B, Sk, Hkv, D), 142), _rand((B, Sk, Hkv, D), 143)
     do = _rand((B, Sq, H, D), 144)
-    bias = _rand((*bshape, Sq, Sk), 145)
+    bias = _rand(_bias_shape(bshape, Sq, Sk), 145)
     o, lse, dq, dk, dv, db = oa.attention_autograd(q, k, v, do, True, 0.5, bias=bias)
     dq2, dk2, dv2, db2 = oa.attention_backward(q, k, v, o, do, lse, True, 0.5, bias=bias)
     assert db.shape == bias.shape
