@@ -62,28 +62,43 @@ int32_t check_span(const int64_t st[4], int32_t S, int32_t D, int es) {
     return span < (1LL << 31) ? FA_OK : FA_ERR_TOO_LARGE;
 }
 
+// The kernels address one (batch, head) slice of the bias / its gradient
+// through a buffer whose 32-bit offsets are (row * i_stride + key) * elem with
+// row < Sq + 256 and key < Sk + 256 (tiles overhang the sequences).
+int32_t check_slice_offsets(const int64_t st[4], int32_t Sq, int32_t Sk, int es) {
+    const int64_t rows = (int64_t)(Sq > 0 ? Sq : 1) + 256;
+    return (rows * st[2] + Sk + 256) * es < (1LL << 31) ? FA_OK : FA_ERR_TOO_LARGE;
+}
+
+// bytes of one (batch, head) slice: rows [0, Sq) of Sk keys
+int32_t slice_span(const int64_t st[4], int32_t Sq, int32_t Sk, int es) {
+    return Sq > 0 ? (int32_t)(((int64_t)(Sq - 1) * st[2] + Sk) * es) : 0;
+}
+
 // Optional bias: element type = the input dtype or float32; (b, h, i, j)
 // strides, j stride 1, the others non-negative multiples of 16 bytes (zero
 // broadcasts), base 16-byte aligned; the kernels read 4 consecutive keys of a
 // row with one 8- or 16-byte load.
-int32_t check_bias(const void* bias, const int64_t st[4], int32_t bias_dtype, int32_t dtype) {
+int32_t check_bias(const void* bias, const int64_t st[4], int32_t bias_dtype, int32_t dtype, int32_t Sq,
+                   int32_t Sk) {
     if (!bias) return FA_OK;
     if (bias_dtype != dtype && bias_dtype != FA_DTYPE_F32) return FA_ERR_BIAS;
     const int es = elem_size(bias_dtype);
     if (!aligned16(bias) || st[3] != 1) return FA_ERR_BIAS;
     for (int i = 0; i < 3; ++i)
         if (st[i] < 0 || (st[i] * es) % 16 != 0) return FA_ERR_BIAS;
-    return FA_OK;
+    return check_slice_offsets(st, Sq, Sk, es);
 }
 
-// Optional bias gradient (float32): j stride 1, 4-byte aligned base,
-// non-negative strides (the kernels store one float per (query, key)).
-int32_t check_dbias(const float* dbias, const int64_t st[4]) {
+// Optional bias gradient (float32): j stride 1, i stride >= Sk (rows do not
+// overlap: stores past the last row must leave the slice), 4-byte aligned
+// base, non-negative strides.
+int32_t check_dbias(const float* dbias, const int64_t st[4], int32_t Sq, int32_t Sk) {
     if (!dbias) return FA_OK;
-    if (((uintptr_t)dbias & 3u) || st[3] != 1) return FA_ERR_BIAS;
+    if (((uintptr_t)dbias & 3u) || st[3] != 1 || st[2] < Sk) return FA_ERR_BIAS;
     for (int i = 0; i < 3; ++i)
         if (st[i] < 0) return FA_ERR_BIAS;
-    return FA_OK;
+    return check_slice_offsets(st, Sq, Sk, 4);
 }
 
 // Backward workspace: B * H rows of 2 * sq_pad float32 (LSE * log2 e, then
@@ -142,7 +157,7 @@ int32_t fa_fwd_check(const fa_fwd_args* a) {
         (st = check_span(a->v_stride, a->seqlen_k, a->head_dim, es)) ||
         (st = check_span(a->o_stride, a->seqlen_q, a->head_dim, es)))
         return st;
-    return check_bias(a->bias, a->bias_stride, a->bias_dtype, a->dtype);
+    return check_bias(a->bias, a->bias_stride, a->bias_dtype, a->dtype, a->seqlen_q, a->seqlen_k);
 }
 
 int32_t fa_fwd(const fa_fwd_args* a, void* stream) {
@@ -176,6 +191,7 @@ int32_t fa_fwd(const fa_fwd_args* a, void* stream) {
     p.bias_sb = a->bias_stride[0];
     p.bias_sh = a->bias_stride[1];
     p.bias_ss = a->bias_stride[2];
+    p.bias_span = a->bias ? slice_span(a->bias_stride, a->seqlen_q, a->seqlen_k, elem_size(a->bias_dtype)) : 0;
     const bool causal = a->causal != 0;
     const bool dropout = a->dropout_p > 0.f;
     hipStream_t s = (hipStream_t)stream;
@@ -230,8 +246,8 @@ int32_t fa_bwd_check(const fa_bwd_args* a, size_t ws_bytes) {
     for (int i = 0; i < 8; ++i)
         if ((st = check_span(strides[i], rows[i], a->head_dim, es))) return st;
     if (a->dbias && !a->bias) return FA_ERR_BIAS;
-    if ((st = check_bias(a->bias, a->bias_stride, a->bias_dtype, a->dtype)) ||
-        (st = check_dbias(a->dbias, a->dbias_stride)))
+    if ((st = check_bias(a->bias, a->bias_stride, a->bias_dtype, a->dtype, a->seqlen_q, a->seqlen_k)) ||
+        (st = check_dbias(a->dbias, a->dbias_stride, a->seqlen_q, a->seqlen_k)))
         return st;
     const size_t need = fa_bwd_workspace_size(a);
     if (need > 0 && ws_bytes < need) return FA_ERR_WORKSPACE;
@@ -285,10 +301,12 @@ int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int
     p.bias_sb = a->bias_stride[0];
     p.bias_sh = a->bias_stride[1];
     p.bias_ss = a->bias_stride[2];
+    p.bias_span = a->bias ? slice_span(a->bias_stride, a->seqlen_q, a->seqlen_k, elem_size(a->bias_dtype)) : 0;
     p.dbias = a->dbias;
     p.dbias_sb = a->dbias_stride[0];
     p.dbias_sh = a->dbias_stride[1];
     p.dbias_ss = a->dbias_stride[2];
+    p.dbias_span = a->dbias ? slice_span(a->dbias_stride, a->seqlen_q, a->seqlen_k, 4) : 0;
     const bool causal = a->causal != 0;
     const bool dropout = a->dropout_p > 0.f;
     hipStream_t s = (hipStream_t)stream;

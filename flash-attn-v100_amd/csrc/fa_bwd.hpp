@@ -105,7 +105,7 @@ struct DkdvCfg {
 
 // TB: element type of the additive bias (T or float), void = no bias
 template <typename T, int D, bool CAUSAL, bool DROPOUT, typename TB>
-__global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const int n_ktiles) {
+__global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_kernel(const BwdParams p, const int n_ktiles) {
     using C = DkdvCfg<T, D>;
     constexpr bool BIAS = !std::is_void<TB>::value;
     using BT = typename std::conditional<BIAS, TB, T>::type;
@@ -215,19 +215,41 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
     };
 
     // ---- bias of this lane's key for the 16 queries {8 g + 4 hi + e} of a sub-step ----
-    constexpr int NBI = BIAS ? 16 : 1;
-    bias1_t<BT> braw[NBI];
-    const int kjc = min(kj, p.Sk - 1);  // keys past Sk are clamped into range (never stored)
+    // one per-lane offset (key, row parity); the query rows go in the scalar
+    // offset.  Rows past Sq read zeros (P = 0 there anyway); lanes past Sk read
+    // zeros or another row and are never stored.
+    // 16-bit values are kept two to a register (rows r, r + 1)
+    constexpr bool B16 = BIAS && !Elem<BT>::kF32;
+    constexpr int NBI = BIAS ? (B16 ? 8 : 16) : 1;
+    using BR = typename std::conditional<B16, s16x2, float>::type;
+    BR braw[NBI];
+    const int bvoff = (4 * hi * (int)p.bias_ss + kj) * (int)sizeof(BT);
     auto load_bias = [&](int it, int st) FA_INLINE {
         if constexpr (BIAS) {
-            const BT* bcol = (const BT*)p.bias + b * p.bias_sb + tile_head(it) * p.bias_sh + kjc;
+            const __amdgpu_buffer_rsrc_t rs =
+                slice_buffer((const BT*)p.bias + b * p.bias_sb + tile_head(it) * p.bias_sh, p.bias_span);
             const int qb0 = tile_q0(it) + 32 * st;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int q = min(qb0 + 8 * (r >> 2) + 4 * hi + (r & 3), p.Sq - 1);
-                braw[r] = load_bias1(bcol + (int64_t)q * p.bias_ss);
+                const auto x = load_bias1<BT>(rs, bvoff, (qb0 + 8 * (r >> 2) + (r & 3)) * (int)p.bias_ss * (int)sizeof(BT));
+                if constexpr (B16)
+                    braw[r >> 1][r & 1] = x;
+                else
+                    braw[r] = x;
             }
         }
+    };
+    auto bias_at = [&](int r) FA_INLINE {
+        if constexpr (B16)
+            return braw[r >> 1][r & 1];
+        else
+            return braw[r];
+    };
+    // dBias stores: lanes past Sk are sent out of range; rows past Sq land past
+    // the slice (query stride >= Sk) and are dropped
+    const int dbvoff = kj < p.Sk ? (4 * hi * (int)p.dbias_ss + kj) * 4 : kOffNowhere;
+    auto dbias_buf = [&](int hh) FA_INLINE {
+        return slice_buffer(p.dbias + b * p.dbias_sb + hh * p.dbias_sh, p.dbias_span);
     };
 
     // ---- P and dS of tile `it` (buffer s); dS = P (dP - delta), scale applied at the end ----
@@ -239,8 +261,8 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
         const float* lse2 = (const float*)(buf(s) + 2 * C::QALLOC) + 32 * st;
         const float* dels = lse2 + BQ;
         const int qb0 = tile_q0(it) + 32 * st;
-        float* dbcol = nullptr;
-        if (BIAS && p.dbias) dbcol = p.dbias + b * p.dbias_sb + tile_head(it) * p.dbias_sh + kj;
+        const bool want_db = BIAS && p.dbias != nullptr;
+        const __amdgpu_buffer_rsrc_t dbrs = dbias_buf(tile_head(it));
         uint64_t col_ctr = 0;
         if (DROPOUT)
             col_ctr = p.offset + (uint64_t)(b * p.H + tile_head(it)) * (uint64_t)p.Sq * (uint64_t)p.Sk + (uint64_t)kj;
@@ -254,7 +276,7 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
                 const int q = qb0 + 8 * g + 4 * hi + e;
                 float pv;
                 if constexpr (BIAS)
-                    pv = fast_exp2(__builtin_fmaf(sc[r], c, bias_log2<BT>(braw[r]) - l4[e]));
+                    pv = fast_exp2(__builtin_fmaf(sc[r], c, __builtin_fmaf(bias_f32<BT>(bias_at(r)), kLog2e, -l4[e])));
                 else
                     pv = fast_exp2(__builtin_fmaf(sc[r], c, -l4[e]));
                 if (MASK && q < kj) pv = 0.f;
@@ -268,8 +290,12 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
                 }
                 pd[r] = pdv;
                 ds[r] = pv * (dpv - d4[e]);
-                if (BIAS && dbcol && q < p.Sq && kj < p.Sk) dbcol[(int64_t)q * p.dbias_ss] = ds[r];
             }
+        }
+        if (want_db) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                store_f32(dbrs, ds[r], dbvoff, (qb0 + 8 * (r >> 2) + (r & 3)) * (int)p.dbias_ss * 4);
         }
         if constexpr (!C::F32) {
 #pragma unroll
@@ -337,6 +363,17 @@ __global__ __launch_bounds__(256, 2) void dkdv_kernel(const BwdParams p, const i
         }
         bcur ^= 1;
     };
+    // dBias rows of query tiles the causal loop skips (queries before the first
+    // visited tile) are zero; the visited tiles write every other row
+    if (BIAS && CAUSAL && p.dbias != nullptr) {
+        const int zrows = min(qt_begin * BQ, p.Sq);
+        for (int g = 0; g < p.group; ++g) {
+            const __amdgpu_buffer_rsrc_t rs = dbias_buf(hk * p.group + g);
+            const int voff = kj < p.Sk ? (hi * (int)p.dbias_ss + kj) * 4 : kOffNowhere;
+            for (int q = 0; q < zrows; q += 2) store_f32(rs, 0.f, voff, q * (int)p.dbias_ss * 4);
+        }
+    }
+
     // masked tiles first for each query head of the group, then plain ones
     int it = 0;
     for (int g = 0; g < p.group; ++g) {
@@ -488,10 +525,11 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
     int bcur = 0;
     if (n_tiles > 0) issue(0, 0);
 
-    // bias of this lane's query row (rows past Sq clamped into range, never stored)
-    const BT* brow = nullptr;
-    if constexpr (BIAS)
-        brow = (const BT*)p.bias + b * p.bias_sb + h * p.bias_sh + (int64_t)min(qi, p.Sq - 1) * p.bias_ss;
+    // bias of this lane's query row (rows past Sq read zeros, keys past Sk read
+    // zeros or the next row: both masked)
+    const __amdgpu_buffer_rsrc_t brs =
+        slice_buffer((const BT*)p.bias + b * p.bias_sb + h * p.bias_sh, BIAS ? p.bias_span : 0);
+    const int bvoff = (qi * (int)p.bias_ss + 4 * hi) * (int)sizeof(BT);
 
     // one 32-key sub-step of the tile in buffer `bcur` starting at key k0
     auto sub = [&](int k0, const T* Ks, const T* Vs, auto mask_tag) FA_INLINE {
@@ -502,9 +540,16 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
             // bias of keys {8 g + 4 hi + 0..3}
             bias4_t<BT> bv[BIAS ? 4 : 1];
             if constexpr (BIAS) {
-                const bool full = k0 + BN <= p.Sk;
+                // tiles of plain steps are whole
+                auto load_all = [&](auto full_tag) FA_INLINE {
 #pragma unroll
-                for (int g = 0; g < 4; ++g) bv[g] = load_bias4(brow, k0 + 8 * g + 4 * hi, p.Sk, full);
+                    for (int g = 0; g < 4; ++g)
+                        bv[g] = load_bias4<BT, decltype(full_tag)::value>(brs, bvoff, (k0 + 8 * g) * (int)sizeof(BT));
+                };
+                if (!MASK || k0 + BN <= p.Sk)
+                    load_all(std::true_type{});
+                else
+                    load_all(std::false_type{});
             }
             // ---- S^T = K Q^T, dP^T = V dO^T (C[key][query]) ----
             f32x16 s = f32x16{}, dp = f32x16{};
@@ -539,7 +584,7 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
                 const int key = k0 + 8 * (r >> 2) + 4 * hi + (r & 3);
                 float pv;
                 if constexpr (BIAS)
-                    pv = fast_exp2(__builtin_fmaf(s[r], c, bias_log2<BT>(bv[r >> 2][r & 3]) - lse2));
+                    pv = fast_exp2(__builtin_fmaf(s[r], c, __builtin_fmaf(bias_f32<BT>(bv[r >> 2][r & 3]), kLog2e, -lse2)));
                 else
                     pv = fast_exp2(__builtin_fmaf(s[r], c, -lse2));
                 if (need_mask && (key >= p.Sk || (CAUSAL && key > qi))) pv = 0.f;

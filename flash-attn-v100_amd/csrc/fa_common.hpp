@@ -25,6 +25,7 @@ typedef __bf16 bf16;
 typedef _Float16 f16;
 typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -106,39 +107,63 @@ __device__ FA_INLINE inline float fast_exp2(float x) { return __builtin_amdgcn_e
 template <typename T>
 using bias4_t = typename std::conditional<Elem<T>::kF32, f32x4, s16x4>::type;
 
-// keys key .. key+3 of `row`; when !full, keys >= Sk read as 0 (their scores
-// are masked) and are not touched
+// A (batch, head) slice of the bias (or of its gradient) is addressed through
+// a buffer resource whose range is the slice's byte span: reads past it
+// return 0 and writes past it are dropped, so per-lane offsets need no bounds
+// checks and stay 32-bit (the host bounds every offset below 2^31).
 template <typename T>
-__device__ FA_INLINE inline bias4_t<T> load_bias4(const T* row, int key, int Sk, bool full) {
-    using V = bias4_t<T>;
-    if (full) return *reinterpret_cast<const V*>(row + key);
-    V v;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        if constexpr (Elem<T>::kF32)
-            v[e] = key + e < Sk ? row[key + e] : 0.f;
-        else
-            v[e] = key + e < Sk ? __builtin_bit_cast(short, row[key + e]) : (short)0;
-    }
-    return v;
+__device__ FA_INLINE inline __amdgpu_buffer_rsrc_t slice_buffer(const T* base, int span_bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, span_bytes, 0x00020000);
 }
 
-// raw bias element -> bias * log2(e)
+// Four consecutive keys at byte offset voff + soff.  full: one 8- or 16-byte
+// load.  A load that straddles the end of the range reads as all zeros, so a
+// tile that holds the last key of a row (the last row of a slice may end
+// inside a group of four) loads key by key instead.
+template <typename T, bool FULL>
+__device__ FA_INLINE inline bias4_t<T> load_bias4(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
+    if constexpr (FULL) {
+        if constexpr (Elem<T>::kF32)
+            return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0));
+        else
+            return __builtin_bit_cast(s16x4, __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, 0));
+    } else {
+        bias4_t<T> v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if constexpr (Elem<T>::kF32)
+                v[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff + 4 * e, 0));
+            else
+                v[e] = (short)__builtin_amdgcn_raw_buffer_load_b16(rs, voff, soff + 2 * e, 0);
+        }
+        return v;
+    }
+}
+
+// raw bias element -> float
 template <typename T>
-__device__ FA_INLINE inline float bias_log2(float x) { return x * kLog2e; }
+__device__ FA_INLINE inline float bias_f32(float x) { return x; }
 template <typename T>
-__device__ FA_INLINE inline float bias_log2(short x) { return Elem<T>::unpack1(x) * kLog2e; }
+__device__ FA_INLINE inline float bias_f32(short x) { return Elem<T>::unpack1(x); }
 
 // one raw bias element (16-bit types as short)
 template <typename T>
 using bias1_t = typename std::conditional<Elem<T>::kF32, float, short>::type;
 template <typename T>
-__device__ FA_INLINE inline bias1_t<T> load_bias1(const T* p) {
+__device__ FA_INLINE inline bias1_t<T> load_bias1(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
     if constexpr (Elem<T>::kF32)
-        return *p;
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff, 0));
     else
-        return __builtin_bit_cast(short, *p);
+        return (short)__builtin_amdgcn_raw_buffer_load_b16(rs, voff, soff, 0);
 }
+
+// one float32 store at byte offset voff + soff (dropped past the range)
+__device__ FA_INLINE inline void store_f32(__amdgpu_buffer_rsrc_t rs, float x, int voff, int soff) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, x), rs, voff, soff, 0);
+}
+// a lane offset that lands every access of the lane out of range (offsets
+// past it stay below 2^32, so they cannot wrap back into the range)
+constexpr int kOffNowhere = (int)0x80000000u;
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also fences global
 // memory, which on gfx9 (one counter for vector loads and stores) makes every

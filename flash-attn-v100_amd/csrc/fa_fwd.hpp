@@ -21,9 +21,9 @@
 //     run the masking variant of the tile step.
 //   * fp32 inputs use v_mfma_f32_32x32x2_f32 with fp32 P.
 //   * optional additive bias (BIAS): each lane reads 4 consecutive keys of its
-//     query's bias row per load, issued with the tile's S MFMAs; the scores
-//     then become t = S * scale * log2 e + bias * log2 e (one FMA) before the
-//     mask, and the softmax runs on t (reference forward_kernel.py:166-182).
+//     query's bias row per load, issued a tile ahead; the scores become
+//     t = S * scale + bias (one FMA) before the mask, and the softmax runs on
+//     t with log2 e as its factor (reference forward_kernel.py:166-182).
 #pragma once
 
 #include <type_traits>
@@ -104,31 +104,40 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     float m_run = -1e30f;  // running max in log2 units (scores * scale * log2 e)
     float l_run = 0.f;     // lane-partial row sum of exp2(t - m_run)
     float m_raw = -INFINITY;
-    // score -> log2 units; with a bias the scores are converted (and the bias
-    // added) before the max, so the softmax factor is 1
-    const float c = BIAS ? 1.f : p.scale_log2;
+    // score -> log2 units; with a bias the scores are scaled (and the bias
+    // added) before the max, so the softmax factor is log2 e
+    const float c = BIAS ? kLog2e : p.scale_log2;
 
     // ---- bias: 4-key groups {32 blk + 8 g + 4 hi + 0..3} of this lane's row ----
+    // (rows past Sq read zeros; keys past Sk read zeros or the next row: masked)
     constexpr int NG = BIAS ? NB * 4 : 1;
     bias4_t<BT> bv[NG];
-    const BT* brow = nullptr;
-    if constexpr (BIAS)  // rows past Sq are clamped into range (never stored)
-        brow = (const BT*)p.bias + b * p.bias_sb + h * p.bias_sh + (int64_t)min(qi, p.Sq - 1) * p.bias_ss;
-    auto load_bias = [&](int k0) FA_INLINE {
+    const __amdgpu_buffer_rsrc_t brs =
+        slice_buffer((const BT*)p.bias + b * p.bias_sb + h * p.bias_sh, BIAS ? p.bias_span : 0);
+    const int bvoff = (qi * (int)p.bias_ss + 4 * hi) * (int)sizeof(BT);
+    // a tile of plain iterations is always whole (MAYBE_TAIL = false)
+    auto load_bias = [&](int k0, auto tail_tag) FA_INLINE {
         if constexpr (BIAS) {
-            const bool full = k0 + BN <= p.Sk;
+            auto load_all = [&](auto full_tag) FA_INLINE {
 #pragma unroll
-            for (int g = 0; g < NG; ++g) bv[g] = load_bias4(brow, k0 + 32 * (g >> 2) + 8 * (g & 3) + 4 * hi, p.Sk, full);
+                for (int g = 0; g < NG; ++g)
+                    bv[g] = load_bias4<BT, decltype(full_tag)::value>(
+                        brs, bvoff, (k0 + 32 * (g >> 2) + 8 * (g & 3)) * (int)sizeof(BT));
+            };
+            if (!decltype(tail_tag)::value || k0 + BN <= p.Sk)
+                load_all(std::true_type{});
+            else
+                load_all(std::false_type{});
         }
     };
-    // t = S * scale * log2 e + bias * log2 e
+    // t = S * scale + bias
     auto add_bias = [&](f32x16 (&s)[NB]) FA_INLINE {
         if constexpr (BIAS) {
 #pragma unroll
             for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
-                    s[blk][r] = __builtin_fmaf(s[blk][r], p.scale_log2, bias_log2<BT>(bv[4 * blk + (r >> 2)][r & 3]));
+                    s[blk][r] = __builtin_fmaf(s[blk][r], p.scale, bias_f32<BT>(bv[4 * blk + (r >> 2)][r & 3]));
         }
     };
 
@@ -300,7 +309,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     }
     sync_tiles();
     if (n_w > 0) {
-        load_bias(0);
+        load_bias(0, std::true_type{});
         qk(Ks0, sa);
         add_bias(sa);
         if (n_plain == 0) mask(sa, 0);
@@ -316,7 +325,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
         const bool next = !MASK || j + 1 < n_w;
         if (act) {
             if (next) {
-                load_bias((j + 1) * BN);
+                load_bias((j + 1) * BN, mask_tag);
                 qk(Ks0 + ((j + 1) & 1) * C::KTILE, sn);
             }
             softmax(sc, pk, j * BN);
@@ -355,7 +364,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     if (hi == 0 && qi < p.Sq) {
         const int64_t si = (int64_t)(b * p.H + h) * p.Sq + qi;
         p.lse[si] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
-        if (p.mx) p.mx[si] = m_raw * (BIAS ? kLn2 : p.scale);
+        if (p.mx) p.mx[si] = BIAS ? m_raw : m_raw * p.scale;
     }
     sync_tiles();  // all waves done with the K/V buffers and no copy still in flight
     constexpr int OW = C::OW;

@@ -30,6 +30,7 @@ struct FwdParams {
     // zero stride broadcasts that dimension, the key stride is 1
     const void* bias;
     int64_t bias_sb, bias_sh, bias_ss;
+    int bias_span;  // bytes of one (batch, head) slice: ((Sq - 1) * ss + Sk) * elem
 };
 
 struct BwdParams {
@@ -61,8 +62,10 @@ struct BwdParams {
     uint64_t seed, offset;
     const void* bias;  // as in FwdParams
     int64_t bias_sb, bias_sh, bias_ss;
+    int bias_span;
     float* dbias;      // optional fp32 (B, H, Sq, Sk) gradient of the bias, key stride 1
-    int64_t dbias_sb, dbias_sh, dbias_ss;
+    int64_t dbias_sb, dbias_sh, dbias_ss;  // query stride >= Sk
+    int dbias_span;    // bytes of one (batch, head) slice
 };
 
 // per-(batch, head) rows of the backward workspace are padded to a multiple

@@ -279,9 +279,8 @@ def bwd(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float = 0.0,
     dbias = None
     if want_dbias:
         B, Sq, H, _ = q.shape
-        # causal: (query, key) pairs of tiles the kernels skip keep their zero
-        alloc = torch.zeros if causal else torch.empty
-        dbias = alloc((B, H, Sq, k.shape[1]), device=q.device, dtype=torch.float32)
+        # every element is written by the kernels (zeros where causal masks)
+        dbias = torch.empty((B, H, Sq, k.shape[1]), device=q.device, dtype=torch.float32)
     a = bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, offset, pb, dbias)
     ws_bytes = lib.fa_bwd_workspace_size(ctypes.byref(a))
     ws = torch.empty(max(int(ws_bytes), 256), device=q.device, dtype=torch.uint8)

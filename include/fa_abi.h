@@ -53,7 +53,8 @@ extern "C" {
 #define FA_ERR_LAUNCH -11     /* the HIP runtime rejected a kernel launch */
 #define FA_ERR_TOO_LARGE -12  /* a grid dimension would overflow, or max(S, 256) rows
                                  of one (batch, head) slice of a tensor span >= 2^31
-                                 bytes (S = its sequence length) */
+                                 bytes (S = its sequence length), or Sq + 256 rows
+                                 of a bias / dbias slice do */
 #define FA_ERR_BIAS -13       /* bias / dbias dtype, strides or alignment violate the rules above */
 
 /* Forward arguments.
@@ -139,8 +140,8 @@ typedef struct fa_bwd_args {
     const void* bias;         /* optional, as in fa_fwd_args */
     int64_t bias_stride[4];
     int32_t bias_dtype;
-    float* dbias;             /* optional float32 (B, H, Sq, Sk) gradient of the bias */
-    int64_t dbias_stride[4];  /* (b, h, i, j) in elements; j stride 1, i stride a multiple of 4 */
+    float* dbias;             /* optional float32 (B, H, Sq, Sk) gradient of the bias, fully written */
+    int64_t dbias_stride[4];  /* (b, h, i, j) in elements; j stride 1, i stride >= Sk */
 } fa_bwd_args;
 
 /* Library ABI version (FA_ABI_VERSION).  No reference counterpart. */
