@@ -12,7 +12,14 @@ roofline of the dominant kernel and the CPU baseline (the reference's PyTorch
 math path restated in oracle/, fp32 on this host, on a bounded sample of the
 same workload) ride along.
 
+With ``--bias full`` (a (B, H, S, S) bf16 additive bias) or ``--bias heads``
+(a (1, H, S, S) one, shared over the batch) the same step runs the bias path of
+the kernels; ``--dbias`` also produces the bias gradient (the fp32 dS written by
+the dK/dV kernel, summed over the batch for ``heads``), inside the timed step.
+The FLOP count is the same (the bias adds no matrix products).
+
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                    [--bias {none,full,heads}] [--dbias]
 """
 from __future__ import annotations
 
@@ -37,7 +44,10 @@ def f_fwd(b=B, h=H, s=S, d=D, causal=CAUSAL):
     return 4.0 * b * h * s * s * d * (0.5 if causal else 1.0)
 
 
-def gpu_bench(steps: int, warmup: int):
+BIAS_SHAPES = {"full": (B, H, S, S), "heads": (1, H, S, S)}
+
+
+def gpu_bench(steps: int, warmup: int, bias_kind: str = "none", want_dbias: bool = False):
     import ctypes
 
     import torch
@@ -52,8 +62,14 @@ def gpu_bench(steps: int, warmup: int):
     o = torch.empty_like(q)
     lse = torch.empty(B, H, S, device="cuda", dtype=torch.float32)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    fa = _lib.fwd_args(q, k, v, o, lse, None, CAUSAL, scale, 0.0, 0, 0)
-    ba = _lib.bwd_args(q, k, v, o, do, lse, dq, dk, dv, CAUSAL, scale, 0.0, 0, 0)
+    pb = dbias = None
+    if bias_kind != "none":
+        bias = torch.randn(BIAS_SHAPES[bias_kind], device="cuda", dtype=torch.float32).to(torch.bfloat16)
+        pb = _lib.prepare_bias(bias, B, H, S, S, torch.bfloat16)
+        if want_dbias:
+            dbias = torch.empty(B, H, S, S, device="cuda", dtype=torch.float32)
+    fa = _lib.fwd_args(q, k, v, o, lse, None, CAUSAL, scale, 0.0, 0, 0, pb)
+    ba = _lib.bwd_args(q, k, v, o, do, lse, dq, dk, dv, CAUSAL, scale, 0.0, 0, 0, pb, dbias)
     ws_bytes = lib.fa_bwd_workspace_size(ctypes.byref(ba))
     ws = torch.empty(ws_bytes, device="cuda", dtype=torch.uint8)
     stream = torch.cuda.current_stream()
@@ -73,6 +89,8 @@ def gpu_bench(steps: int, warmup: int):
     def step():
         fwd()
         bwd_stage(-1)
+        if dbias is not None and bias_kind == "heads":
+            _lib.reduce_dbias(dbias, pb)  # the batch sum the caller's (1, H, S, S) gradient needs
 
     for _ in range(warmup):
         step()
@@ -108,7 +126,7 @@ def gpu_bench(steps: int, warmup: int):
                 fwd_bwd_ms=fwd_bwd_ms, finite=ok, device=torch.cuda.get_device_name(0))
 
 
-def cpu_baseline(target_s: float = 12.0):
+def cpu_baseline(target_s: float = 12.0, bias_kind: str = "none"):
     """The reference's math path (oracle.attention, fp32, autograd backward) on
     this host's cores, on B=1 and as many heads of the workload as fit about
     ``target_s`` seconds; reported with the same algorithmic FLOP count."""
@@ -122,8 +140,9 @@ def cpu_baseline(target_s: float = 12.0):
 
     def run(h):
         q, k, v, do = (torch.randn(1, S, h, D, generator=g, dtype=torch.float32) for _ in range(4))
+        bias = None if bias_kind == "none" else torch.randn(1, h, S, S, generator=g, dtype=torch.float32)
         t0 = time.perf_counter()
-        oa.attention_autograd(q, k, v, do, CAUSAL, D ** -0.5, dtype=torch.float32)
+        oa.attention_autograd(q, k, v, do, CAUSAL, D ** -0.5, dtype=torch.float32, bias=bias)
         return time.perf_counter() - t0
 
     run(1)  # warm-up
@@ -134,7 +153,8 @@ def cpu_baseline(target_s: float = 12.0):
     flop = 3.5 * f_fwd(b=1, h=h)
     return {"value": round(flop / t / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"fwd+bwd of B=1, H={h} of the workload (S=4096, D=128, causal) in fp32 via "
+            "sample": f"fwd+bwd of B=1, H={h} of the workload (S=4096, D=128, causal"
+                      f"{'' if bias_kind == 'none' else ', additive bias with its gradient'}) in fp32 via "
                       f"oracle.attention_autograd; best of 2 runs, {t:.2f} s each",
             "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count()}
 
@@ -150,11 +170,12 @@ def _cpu_model():
     return None
 
 
-def _profiled_traffic(kernel: str):
+def _profiled_traffic(kernel: str, profile: str):
     """HBM bytes per launch of ``kernel`` (read + write) from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this workload, already scaled
-    by the copy calibration; None if the kernel was not profiled."""
-    path = os.path.join(REPO, "profiles", "c3_bf16_causal_traffic.json")
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary ``profiles/<profile>`` of this
+    workload, already scaled by the copy calibration; None if the kernel (or
+    the workload) was not profiled."""
+    path = os.path.join(REPO, "profiles", profile)
     try:
         with open(path) as f:
             k = json.load(f)["kernels"].get(kernel)
@@ -184,6 +205,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--bias", choices=("none", "full", "heads"), default="none",
+                    help="run the additive-bias path: full = (B, H, S, S), heads = (1, H, S, S), bf16")
+    ap.add_argument("--dbias", action="store_true", help="with --bias: also produce the bias gradient")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
     a = ap.parse_args()
@@ -195,7 +219,9 @@ def main():
               "(the reference's multi-GPU helpers are out of scope)", file=sys.stderr)
         sys.exit(2)
 
-    r = gpu_bench(a.steps, a.warmup)
+    if a.dbias and a.bias == "none":
+        ap.error("--dbias needs --bias")
+    r = gpu_bench(a.steps, a.warmup, a.bias, a.dbias)
     F = f_fwd()
     Ftot = 3.5 * F
     value = Ftot / r["t_step"] / 1e12
@@ -206,7 +232,8 @@ def main():
     # (QK^T recompute, dO V^T, P^T dO, dS^T Q); dq = dS K (its S/dP recompute is extra work)
     algo = {"fwd_kernel": F, "dkdv_kernel": 2.0 * F, "dq_kernel": 0.5 * F}
     dom = max(kernels, key=kernels.get)
-    traffic = _profiled_traffic(dom)
+    tag = "" if a.bias == "none" else f"_bias_{a.bias}{'_dbias' if a.dbias else ''}"
+    traffic = _profiled_traffic(dom, f"c3_bf16_causal{tag}_traffic.json")
     if dom in algo:
         ach = algo[dom] / (kernels[dom] * 1e-3) / 1e12
         roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_BF16_TFLOPS,
@@ -230,9 +257,12 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "C3: B=4 S=4096 H=32 D=128 bf16 causal, fwd+bwd (BASELINE configs[2])",
+        "config": {"workload": "C3: B=4 S=4096 H=32 D=128 bf16 causal, fwd+bwd (BASELINE configs[2])"
+                               + ("" if a.bias == "none" else
+                                  f", additive bf16 bias {BIAS_SHAPES[a.bias]}"
+                                  + (" with its gradient" if a.dbias else "")),
                    "batch": B, "seq_len": S, "heads": H, "head_dim": D, "causal": CAUSAL,
-                   "parallelism": "single-gpu"},
+                   "bias": a.bias, "dbias": a.dbias, "parallelism": "single-gpu"},
         "fwd_bwd_tflops": round(value, 2),
         "fwd_bwd_pct_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
         "fwd_tflops": round(fwd_tflops, 2),
@@ -244,7 +274,7 @@ def main():
         "roofline": roof,
     }
     if not a.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline()
+        out["cpu_baseline"] = cpu_baseline(bias_kind=a.bias)
     print(json.dumps(out), flush=True)
 
 
