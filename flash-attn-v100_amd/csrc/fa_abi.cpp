@@ -90,23 +90,52 @@ int32_t check_bias(const void* bias, const int64_t st[4], int32_t bias_dtype, in
     return check_slice_offsets(st, Sq, Sk, es);
 }
 
+// The bias gradient is summed over a dimension whose dbias stride is 0 (batch
+// or head, with more than one of them): the dK/dV kernel then writes
+// per-(batch, head) parts into the workspace and a reduction kernel sums them.
+bool dbias_reduced(const fa_bwd_args* a) {
+    return a->dbias && ((a->dbias_stride[0] == 0 && a->batch > 1) || (a->dbias_stride[1] == 0 && a->num_heads > 1));
+}
+// key row length of the parts: Sk rounded up to 4 (16-byte rows)
+int32_t dbias_part_row(int32_t Sk) { return (Sk + 3) / 4 * 4; }
+
 // Optional bias gradient (float32): j stride 1, i stride >= Sk (rows do not
 // overlap: stores past the last row must leave the slice), 4-byte aligned
-// base, non-negative strides.
-int32_t check_dbias(const float* dbias, const int64_t st[4], int32_t Sq, int32_t Sk) {
+// base, non-negative strides.  Summed form: 16-byte aligned base and strides
+// that are multiples of 4 (16-byte stores of 4 keys).
+int32_t check_dbias(const fa_bwd_args* a) {
+    const float* dbias = a->dbias;
+    const int64_t* st = a->dbias_stride;
     if (!dbias) return FA_OK;
-    if (((uintptr_t)dbias & 3u) || st[3] != 1 || st[2] < Sk) return FA_ERR_BIAS;
+    if (((uintptr_t)dbias & 3u) || st[3] != 1 || st[2] < a->seqlen_k) return FA_ERR_BIAS;
     for (int i = 0; i < 3; ++i)
         if (st[i] < 0) return FA_ERR_BIAS;
-    return check_slice_offsets(st, Sq, Sk, 4);
+    if (dbias_reduced(a)) {
+        if (!aligned16(dbias)) return FA_ERR_BIAS;
+        for (int i = 0; i < 3; ++i)
+            if (st[i] % 4 != 0) return FA_ERR_BIAS;
+        const int64_t part_st[4] = {0, 0, dbias_part_row(a->seqlen_k), 1};
+        if (check_slice_offsets(part_st, a->seqlen_q, a->seqlen_k, 4)) return FA_ERR_TOO_LARGE;
+    }
+    return check_slice_offsets(st, a->seqlen_q, a->seqlen_k, 4);
 }
 
 // Backward workspace: B * H rows of 2 * sq_pad float32 (LSE * log2 e, then
-// delta), sq_pad = Sq rounded up to kSqPad; total rounded up to 256 bytes.
-size_t ws_bytes_for(const fa_bwd_args* a) {
+// delta), sq_pad = Sq rounded up to kSqPad, rounded up to 256 bytes; then,
+// for a summed bias gradient, the (B, H, Sq, Sk rounded up to 4) float32
+// parts, rounded up to 256 bytes.
+size_t ws_rows_bytes(const fa_bwd_args* a) {
     const size_t sq_pad = ((size_t)a->seqlen_q + fa::kSqPad - 1) / fa::kSqPad * fa::kSqPad;
     const size_t n = (size_t)a->batch * (size_t)a->num_heads * 2 * sq_pad * sizeof(float);
     return (n + 255) & ~(size_t)255;
+}
+size_t ws_bytes_for(const fa_bwd_args* a) {
+    size_t n = ws_rows_bytes(a);
+    if (dbias_reduced(a)) {
+        const size_t parts = (size_t)a->batch * a->num_heads * a->seqlen_q * dbias_part_row(a->seqlen_k) * 4;
+        n += (parts + 255) & ~(size_t)255;
+    }
+    return n;
 }
 
 }  // namespace
@@ -247,7 +276,7 @@ int32_t fa_bwd_check(const fa_bwd_args* a, size_t ws_bytes) {
         if ((st = check_span(strides[i], rows[i], a->head_dim, es))) return st;
     if (a->dbias && !a->bias) return FA_ERR_BIAS;
     if ((st = check_bias(a->bias, a->bias_stride, a->bias_dtype, a->dtype, a->seqlen_q, a->seqlen_k)) ||
-        (st = check_dbias(a->dbias, a->dbias_stride, a->seqlen_q, a->seqlen_k)))
+        (st = check_dbias(a)))
         return st;
     const size_t need = fa_bwd_workspace_size(a);
     if (need > 0 && ws_bytes < need) return FA_ERR_WORKSPACE;
@@ -302,26 +331,59 @@ int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int
     p.bias_sh = a->bias_stride[1];
     p.bias_ss = a->bias_stride[2];
     p.bias_span = a->bias ? slice_span(a->bias_stride, a->seqlen_q, a->seqlen_k, elem_size(a->bias_dtype)) : 0;
-    p.dbias = a->dbias;
-    p.dbias_sb = a->dbias_stride[0];
-    p.dbias_sh = a->dbias_stride[1];
-    p.dbias_ss = a->dbias_stride[2];
-    p.dbias_span = a->dbias ? slice_span(a->dbias_stride, a->seqlen_q, a->seqlen_k, 4) : 0;
+    const bool reduce_db = dbias_reduced(a);
+    fa::DbiasReduceParams rp{};
+    if (reduce_db) {  // parts in the workspace, summed into dbias after dK/dV
+        const int SkP = dbias_part_row(a->seqlen_k);
+        const int64_t part_st[4] = {(int64_t)a->num_heads * a->seqlen_q * SkP, (int64_t)a->seqlen_q * SkP, SkP, 1};
+        p.dbias = (float*)((char*)workspace + ws_rows_bytes(a));
+        p.dbias_sb = part_st[0];
+        p.dbias_sh = part_st[1];
+        p.dbias_ss = part_st[2];
+        p.dbias_span = slice_span(part_st, a->seqlen_q, a->seqlen_k, 4);
+        p.dbias_zero_fill = 0;
+        rp.part = p.dbias;
+        rp.out = a->dbias;
+        rp.out_sb = a->dbias_stride[0];
+        rp.out_sh = a->dbias_stride[1];
+        rp.out_ss = a->dbias_stride[2];
+        rp.B = a->batch;
+        rp.H = a->num_heads;
+        rp.Sq = a->seqlen_q;
+        rp.Sk = a->seqlen_k;
+        rp.SkP = SkP;
+        rp.sum_b = a->dbias_stride[0] == 0 && a->batch > 1;
+        rp.sum_h = a->dbias_stride[1] == 0 && a->num_heads > 1;
+        rp.causal = a->causal != 0;
+    } else {
+        p.dbias = a->dbias;
+        p.dbias_sb = a->dbias_stride[0];
+        p.dbias_sh = a->dbias_stride[1];
+        p.dbias_ss = a->dbias_stride[2];
+        p.dbias_span = a->dbias ? slice_span(a->dbias_stride, a->seqlen_q, a->seqlen_k, 4) : 0;
+        p.dbias_zero_fill = 1;
+    }
     const bool causal = a->causal != 0;
     const bool dropout = a->dropout_p > 0.f;
     hipStream_t s = (hipStream_t)stream;
     if (a->bias) {
         const bool b32 = a->bias_dtype == FA_DTYPE_F32;
         const int D = a->head_dim;
+        hipError_t e;
         switch (a->dtype) {
             case FA_DTYPE_BF16:
-                return status_of(b32 ? fa::launch_bwd_bias32_bf16(p, D, causal, dropout, stage, s)
-                                     : fa::launch_bwd_bias_bf16(p, D, causal, dropout, stage, s));
+                e = b32 ? fa::launch_bwd_bias32_bf16(p, D, causal, dropout, stage, s)
+                        : fa::launch_bwd_bias_bf16(p, D, causal, dropout, stage, s);
+                break;
             case FA_DTYPE_F16:
-                return status_of(b32 ? fa::launch_bwd_bias32_f16(p, D, causal, dropout, stage, s)
-                                     : fa::launch_bwd_bias_f16(p, D, causal, dropout, stage, s));
-            default: return status_of(fa::launch_bwd_bias_f32(p, D, causal, dropout, stage, s));
+                e = b32 ? fa::launch_bwd_bias32_f16(p, D, causal, dropout, stage, s)
+                        : fa::launch_bwd_bias_f16(p, D, causal, dropout, stage, s);
+                break;
+            default: e = fa::launch_bwd_bias_f32(p, D, causal, dropout, stage, s);
         }
+        // the summed gradient follows the dK/dV stage (stream order)
+        if (e == hipSuccess && reduce_db && (stage < 0 || stage == 1)) e = fa::launch_dbias_reduce(rp, s);
+        return status_of(e);
     }
     switch (a->dtype) {
         case FA_DTYPE_BF16: return status_of(fa::launch_bwd_bf16(p, a->head_dim, causal, dropout, stage, s));

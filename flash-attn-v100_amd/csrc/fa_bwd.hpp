@@ -365,7 +365,7 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
     };
     // dBias rows of query tiles the causal loop skips (queries before the first
     // visited tile) are zero; the visited tiles write every other row
-    if (BIAS && CAUSAL && p.dbias != nullptr) {
+    if (BIAS && CAUSAL && p.dbias != nullptr && p.dbias_zero_fill) {
         const int zrows = min(qt_begin * BQ, p.Sq);
         for (int g = 0; g < p.group; ++g) {
             const __amdgpu_buffer_rsrc_t rs = dbias_buf(hk * p.group + g);

@@ -1,4 +1,5 @@
-// Test hooks exposing the device RNG exactly as the attention kernels use it.
+// Test hooks exposing the device RNG exactly as the attention kernels use it,
+// and the broadcast reduction of the bias gradient.
 #include "fa_common.hpp"
 #include "fa_params.hpp"
 
@@ -25,6 +26,56 @@ hipError_t launch_dropout_mask(uint64_t seed, uint64_t offset, int B, int H, int
     const int64_t nb = (n + 255) / 256;
     if (nb > 0x7fffffff) return hipErrorInvalidValue;
     hipLaunchKernelGGL(dropout_mask_kernel, dim3((unsigned)nb), dim3(256), 0, s, seed, offset, n, p, keep);
+    return hipGetLastError();
+}
+
+// One thread per 4 consecutive keys of one output row: 16-byte loads of
+// every part slice that sums into it (HBM-bound streaming, no atomics).
+__global__ __launch_bounds__(256) void dbias_reduce_kernel(const DbiasReduceParams r) {
+    const int nj4 = (r.Sk + 3) >> 2;
+    const int Bo = r.sum_b ? 1 : r.B, Ho = r.sum_h ? 1 : r.H;
+    const int64_t n = (int64_t)Bo * Ho * r.Sq * nj4;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= n) return;
+    const int j = (int)(t % nj4) * 4;
+    int64_t rest = t / nj4;
+    const int i = (int)(rest % r.Sq);
+    rest /= r.Sq;
+    const int ho = (int)(rest % Ho), bo = (int)(rest / Ho);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (!r.causal || j <= i) {
+        const int b0 = r.sum_b ? 0 : bo, b1 = r.sum_b ? r.B : bo + 1;
+        const int h0 = r.sum_h ? 0 : ho, h1 = r.sum_h ? r.H : ho + 1;
+        for (int b = b0; b < b1; ++b)
+            for (int h = h0; h < h1; ++h) {
+                const float4 v = *reinterpret_cast<const float4*>(
+                    r.part + (((int64_t)b * r.H + h) * r.Sq + i) * r.SkP + j);
+                acc.x += v.x;
+                acc.y += v.y;
+                acc.z += v.z;
+                acc.w += v.w;
+            }
+        if (r.causal) {  // the part entries past the diagonal were never written
+            if (j + 1 > i) acc.y = 0.f;
+            if (j + 2 > i) acc.z = 0.f;
+            if (j + 3 > i) acc.w = 0.f;
+        }
+    }
+    float* o = r.out + bo * r.out_sb + ho * r.out_sh + (int64_t)i * r.out_ss + j;
+    if (j + 4 <= r.Sk) {
+        *reinterpret_cast<float4*>(o) = acc;
+    } else {
+        const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+        for (int e = 0; e < r.Sk - j; ++e) o[e] = a[e];
+    }
+}
+
+hipError_t launch_dbias_reduce(const DbiasReduceParams& r, hipStream_t s) {
+    const int64_t n = (int64_t)(r.sum_b ? 1 : r.B) * (r.sum_h ? 1 : r.H) * r.Sq * ((r.Sk + 3) / 4);
+    if (n <= 0) return hipSuccess;
+    const int64_t nb = (n + 255) / 256;
+    if (nb > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(dbias_reduce_kernel, dim3((unsigned)nb), dim3(256), 0, s, r);
     return hipGetLastError();
 }
 

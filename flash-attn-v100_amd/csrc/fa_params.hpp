@@ -66,6 +66,20 @@ struct BwdParams {
     float* dbias;      // optional fp32 (B, H, Sq, Sk) gradient of the bias, key stride 1
     int64_t dbias_sb, dbias_sh, dbias_ss;  // query stride >= Sk
     int dbias_span;    // bytes of one (batch, head) slice
+    int dbias_zero_fill;  // causal: also zero the rows of query tiles the loop skips
+};
+
+// Sum of per-(batch, head) dBias slices over broadcast dimensions:
+// out[bo][ho][i][j] = sum of part[b][h][i][j] over b (sum_b) / h (sum_h);
+// part is contiguous (B, H, Sq, SkP) with SkP = Sk rounded up to 4; causal
+// entries (j > i) are written as 0 without being read (the dK/dV kernel
+// leaves the parts of skipped query tiles unwritten).
+struct DbiasReduceParams {
+    const float* part;
+    float* out;
+    int64_t out_sb, out_sh, out_ss;
+    int B, H, Sq, Sk, SkP;
+    int sum_b, sum_h, causal;
 };
 
 // per-(batch, head) rows of the backward workspace are padded to a multiple
@@ -96,5 +110,6 @@ hipError_t launch_bwd_bias32_f16(const BwdParams& p, int D, bool causal, bool dr
 hipError_t launch_dropout_mask(uint64_t seed, uint64_t offset, int B, int H, int Sq, int Sk, float p,
                                uint8_t* keep, hipStream_t s);
 hipError_t launch_rand(uint64_t seed, const uint64_t* ctr, int64_t n, float* u, hipStream_t s);
+hipError_t launch_dbias_reduce(const DbiasReduceParams& r, hipStream_t s);
 
 }  // namespace fa

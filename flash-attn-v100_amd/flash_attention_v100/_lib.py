@@ -260,7 +260,13 @@ def bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, of
         bias.strides if bias is not None else _I64x4(0, 0, 0, 1),
         bias.dtype_code if bias is not None else DTYPE_CODES[q.dtype],
         dbias.data_ptr() if dbias is not None else None,
-        _strides(dbias) if dbias is not None else _I64x4(0, 0, 0, 1))
+        _dbias_strides(dbias) if dbias is not None else _I64x4(0, 0, 0, 1))
+
+
+def _dbias_strides(dbias):
+    # a size-1 batch / head dimension of the gradient buffer asks the library
+    # to sum over that dimension (stride 0)
+    return _I64x4(*[0 if d < 2 and dbias.shape[d] == 1 else dbias.stride(d) for d in range(4)])
 
 
 def bwd(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float = 0.0,
@@ -279,8 +285,16 @@ def bwd(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float = 0.0,
     dbias = None
     if want_dbias:
         B, Sq, H, _ = q.shape
-        # every element is written by the kernels (zeros where causal masks)
-        dbias = torch.empty((B, H, Sq, k.shape[1]), device=q.device, dtype=torch.float32)
+        Sk = k.shape[1]
+        # batch / head dimensions the bias broadcasts are summed by the library;
+        # every element is written (zeros where causal masks).  Summed rows are
+        # 16-byte aligned (padded to 4 keys).
+        Bo = 1 if pb.shape[0] == 1 else B
+        Ho = 1 if pb.shape[1] == 1 else H
+        if (Bo, Ho) == (B, H):
+            dbias = torch.empty((B, H, Sq, Sk), device=q.device, dtype=torch.float32)
+        else:
+            dbias = torch.empty((Bo, Ho, Sq, -(-Sk // 4) * 4), device=q.device, dtype=torch.float32)[..., :Sk]
     a = bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, offset, pb, dbias)
     ws_bytes = lib.fa_bwd_workspace_size(ctypes.byref(a))
     ws = torch.empty(max(int(ws_bytes), 256), device=q.device, dtype=torch.uint8)

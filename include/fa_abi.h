@@ -104,9 +104,11 @@ typedef struct fa_fwd_args {
  * dv in the input dtype (fully overwritten, no zero-init needed).  With a
  * bias, the forward's bias is passed again; if dbias is non-NULL the kernels
  * also write dS = d loss / d(scaled score + bias) into it, float32, logically
- * (B, H, Sq, Sk) with its own (b, h, i, j) strides (no broadcast: a caller
- * with a broadcast bias sums over those dimensions; the reference returned
- * zeros, ops/attention.py:297-301). */
+ * (B, H, Sq, Sk) with its own (b, h, i, j) strides (the reference returned
+ * zeros, ops/attention.py:297-301).  A zero b or h stride of dbias sums the
+ * gradient over that dimension (the gradient of a bias broadcast over it):
+ * the workspace then also holds the per-(b, h) parts, and dbias needs a
+ * 16-byte aligned base and strides that are multiples of 4. */
 typedef struct fa_bwd_args {
     const void* q;
     const void* k;
@@ -141,7 +143,7 @@ typedef struct fa_bwd_args {
     int64_t bias_stride[4];
     int32_t bias_dtype;
     float* dbias;             /* optional float32 (B, H, Sq, Sk) gradient of the bias, fully written */
-    int64_t dbias_stride[4];  /* (b, h, i, j) in elements; j stride 1, i stride >= Sk */
+    int64_t dbias_stride[4];  /* (b, h, i, j) in elements; j stride 1, i stride >= Sk; b, h: 0 = sum */
 } fa_bwd_args;
 
 /* Library ABI version (FA_ABI_VERSION).  No reference counterpart. */
@@ -161,7 +163,9 @@ int32_t fa_fwd(const fa_fwd_args* args, void* hip_stream);
 
 /* Bytes of device workspace fa_bwd needs: B * H rows of 2 * sq_pad float32
  * (sq_pad = Sq rounded up to 128; LSE * log2 e then delta = rowsum(dO * O),
- * written by the pre-pass), rounded up to 256 bytes; 0 on invalid arguments.
+ * written by the pre-pass), rounded up to 256 bytes; plus, for a summed
+ * dbias, B * H * Sq * (Sk rounded up to 4) float32 parts, rounded up to 256
+ * bytes; 0 on invalid arguments.
  * The reference had no workspace (it recomputed delta per tile pair,
  * backward_kernel.py:119-121). */
 size_t fa_bwd_workspace_size(const fa_bwd_args* args);

@@ -275,3 +275,26 @@ def test_reduce_dbias_sums_broadcast_dims():
     r = _lib.reduce_dbias(g, pb)
     assert r.shape == (1, 3, 1, 5) and r.dtype == torch.bfloat16
     assert torch.equal(r.float(), g.sum(dim=(0, 2), keepdim=True).to(torch.bfloat16).float())
+
+
+def test_summed_dbias_workspace_and_rules():
+    # a zero batch/head stride of dbias sums the gradient; the workspace then
+    # also holds the (B, H, Sq, Sk rounded up to 4) float32 parts
+    lib = _lib.load()
+    B, S, H, D, Sk = 2, 100, 3, 64, 98
+    q = torch.zeros(B, S, H, D, dtype=torch.bfloat16)
+    k = torch.zeros(B, Sk, H, D, dtype=torch.bfloat16)
+    lse = torch.zeros(B, H, S)
+    pb = _lib.prepare_bias(torch.zeros(1, H, S, Sk, dtype=torch.bfloat16), B, H, S, Sk, q.dtype)
+    full = torch.zeros(B, H, S, Sk)
+    a = _lib.bwd_args(q, k, k, q, q, lse, q, k, k, True, 0.125, 0.0, 0, 0, pb, full)
+    base = lib.fa_bwd_workspace_size(ctypes.byref(a))
+    summed = torch.zeros(1, H, S, 100)[..., :Sk]
+    a = _lib.bwd_args(q, k, k, q, q, lse, q, k, k, True, 0.125, 0.0, 0, 0, pb, summed)
+    assert list(a.dbias_stride) == [0, S * 100, 100, 1]
+    ws = lib.fa_bwd_workspace_size(ctypes.byref(a))
+    assert ws == base + ((B * H * S * 100 * 4 + 255) // 256) * 256
+    assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_OK"]
+    assert lib.fa_bwd_check(ctypes.byref(a), base) == CODES["FA_ERR_WORKSPACE"]
+    a.dbias_stride[2] = 99  # summed rows must hold 16-byte groups of keys
+    assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_ERR_BIAS"]

@@ -83,6 +83,11 @@ CASES += [
     # grouped KV heads
     (torch.bfloat16, 2, 160, 160, 4, 2, 128, True, (2, 4, 160, 160), None),
     (torch.float16, 1, 96, 96, 8, 1, 64, False, (1, 8, 96, 96), None),
+    # gradients summed by the library over batch and/or heads, ragged keys (Sk % 4 != 0)
+    (torch.bfloat16, 2, 99, 150, 2, 2, 64, True, (1, 1, 99, 150), None),
+    (torch.float16, 3, 70, 70, 4, 2, 128, True, (1, 4, 70, 70), None),
+    (torch.float32, 2, 64, 93, 3, 3, 32, False, (2, 1, 64, 93), None),
+    (torch.bfloat16, 2, 130, 131, 4, 1, 64, True, (2, 1, 1, 131), torch.float32),
     # single query / key
     (torch.bfloat16, 1, 1, 1, 2, 2, 64, True, (1, 2, 1, 1), None),
     (torch.float16, 3, 1, 50, 2, 2, 32, False, (3, 2, 1, 50), None),
