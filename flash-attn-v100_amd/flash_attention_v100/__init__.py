@@ -20,6 +20,9 @@ from .ops.attention import (  # noqa: F401
     EnhancedFlashAttentionV100Function,
     FlashAttentionV100Function,
     SUPPORTED_DTYPES,
+    compare_with_pytorch_attention,
+    flash_attention_backward,
+    flash_attention_forward,
 )
 
 __version__ = "0.1.0"
@@ -35,4 +38,7 @@ __all__ = [
     "FlashAttentionExtensionError",
     "FlashAttentionKernelError",
     "SUPPORTED_DTYPES",
+    "flash_attention_forward",
+    "flash_attention_backward",
+    "compare_with_pytorch_attention",
 ]

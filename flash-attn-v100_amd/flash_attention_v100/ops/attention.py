@@ -23,7 +23,8 @@ hints, the gfx950 tile shape is fixed per (dtype, head_dim).
 """
 from __future__ import annotations
 
-from typing import Optional
+import contextlib
+from typing import Any, Dict, Optional, Tuple
 
 import torch
 
@@ -144,3 +145,167 @@ class EnhancedFlashAttentionV100Function(torch.autograd.Function):
 
 
 FlashAttentionV100Function = EnhancedFlashAttentionV100Function
+
+
+# ---------------------------------------------------------------------------
+# Standalone functions (reference ops/attention.py:464-718) and their aliases
+
+def _standalone_inputs(q, k, v, scale, dropout_p, enable_multi_gpu, kwargs):
+    if enable_multi_gpu and torch.distributed.is_available() and torch.distributed.is_initialized() \
+            and torch.distributed.get_world_size() > 1:
+        raise NotImplementedError("multi-GPU execution is out of scope for this single-GPU build")
+    check_block_sizes(kwargs.get("block_size_m"), kwargs.get("block_size_n"))
+    _check_kernel_inputs(q, k, v, dropout_p)
+    return q.shape[-1] ** -0.5 if scale is None else scale
+
+
+def flash_attention_forward_enhanced(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    scale: Optional[float] = None,
+    causal: bool = False,
+    dropout_p: float = 0.0,
+    bias: Optional[torch.Tensor] = None,
+    enable_multi_gpu: bool = False,
+    performance_mode: str = "balanced",
+    **kwargs,
+) -> torch.Tensor:
+    """Forward only, no autograd graph (reference ``ops/attention.py:464-536``):
+    returns O (B, Sq, H, D).  ``dropout_seed`` / ``dropout_offset`` keyword
+    arguments pin the dropout stream; ``block_size_m/n`` are validated hints."""
+    scale = _standalone_inputs(q, k, v, scale, dropout_p, enable_multi_gpu, kwargs)
+    pb = _prepare_bias(bias, q, k)
+    seed, offset = (_lib.seed_offset(kwargs.get("dropout_seed"), kwargs.get("dropout_offset"))
+                    if dropout_p > 0 else (0, 0))
+    with torch.no_grad():
+        o, _, _ = _lib.fwd(q, k, v, causal, scale, dropout_p, seed, offset, bias=pb)
+    return o
+
+
+def flash_attention_backward_enhanced(
+    grad_output: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    output: torch.Tensor,
+    lse: torch.Tensor,
+    max_vals: Optional[torch.Tensor],
+    scale: float,
+    causal: bool = False,
+    enable_multi_gpu: bool = False,
+    **kwargs,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(dQ, dK, dV) from the saved forward state (reference
+    ``ops/attention.py:539-600``).  ``lse`` is the LSE this library's forward
+    returned; ``max_vals`` is not needed.  A forward that used dropout or a
+    bias passes the same ``dropout_p`` / ``dropout_seed`` / ``dropout_offset``
+    / ``bias`` as keyword arguments."""
+    dropout_p = float(kwargs.get("dropout_p", 0.0))
+    scale = _standalone_inputs(q, k, v, scale, dropout_p, enable_multi_gpu, kwargs)
+    if dropout_p > 0 and kwargs.get("dropout_seed") is None:
+        raise ValueError("dropout backward needs the forward's dropout_seed (and dropout_offset)")
+    seed, offset = (_lib.seed_offset(kwargs.get("dropout_seed"), kwargs.get("dropout_offset"))
+                    if dropout_p > 0 else (0, 0))
+    pb = _prepare_bias(kwargs.get("bias"), q, k)
+    return _lib.bwd(q, k, v, output, grad_output, lse, causal, scale, dropout_p, seed, offset, bias=pb)
+
+
+def _reference_attention_fp32(q, k, v, scale, causal, bias, keep, dropout_p):
+    """softmax(Q K^T * scale + bias, causal) [* keep / (1 - p)] V in float32 on the
+    tensors' device, (B, S, H, D) in and out (the math of reference
+    tests/test_attention.py:39-79)."""
+    H = q.shape[2]
+    rep = H // k.shape[2]
+    qf = q.float().transpose(1, 2).contiguous()
+    kf = k.float().repeat_interleave(rep, dim=2).transpose(1, 2).contiguous()
+    vf = v.float().repeat_interleave(rep, dim=2).transpose(1, 2).contiguous()
+    s = torch.matmul(qf, kf.transpose(-2, -1).contiguous()) * scale
+    if bias is not None:
+        s = s + bias.float()
+    if causal:
+        m = torch.triu(torch.ones(s.shape[-2], s.shape[-1], device=s.device, dtype=torch.bool), diagonal=1)
+        s = s.masked_fill(m, float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    if keep is not None:
+        p = p * keep.float() / (1.0 - dropout_p)
+    return torch.matmul(p, vf).transpose(1, 2)
+
+
+def compare_with_pytorch_attention_enhanced(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    causal: bool = False,
+    bias: Optional[torch.Tensor] = None,
+    dropout_p: float = 0.0,
+    atol: float = 1e-4,
+    rtol: float = 1e-4,
+) -> Dict[str, Any]:
+    """The kernels' forward against PyTorch math on the same device, with the
+    reference's report keys (``ops/attention.py:603-718``).  The PyTorch side
+    runs in float32 (no low-precision batched products) and, for dropout,
+    applies the kernels' own keep mask (``fa_dropout_mask``) so that the two
+    outputs are comparable element by element; the reference passed dropout
+    to SDPA's independent RNG instead."""
+    _check_kernel_inputs(q, k, v, dropout_p)
+    scale = q.shape[-1] ** -0.5
+    seed, offset = _lib.seed_offset(None, None) if dropout_p > 0 else (0, 0)
+    flash = flash_attention_forward_enhanced(q, k, v, scale, causal, dropout_p, bias,
+                                             dropout_seed=seed, dropout_offset=offset)
+    keep = None
+    if dropout_p > 0:
+        B, Sq, H, _ = q.shape
+        keep = _lib.dropout_mask(seed, offset, B, H, Sq, k.shape[1], dropout_p, device=q.device)
+    with torch.no_grad():
+        ref = _reference_attention_fp32(q, k, v, scale, causal, bias, keep, dropout_p)
+    f = flash.float()
+    abs_diff = (f - ref).abs()
+    rel_diff = abs_diff / (ref.abs() + 1e-8)
+
+    def stats(t):
+        return {"mean": t.mean().item(), "std": t.std().item(), "min": t.min().item(), "max": t.max().item()}
+
+    return {
+        "allclose": bool(torch.allclose(f, ref, atol=atol, rtol=rtol)),
+        "max_absolute_difference": abs_diff.max().item(),
+        "mean_absolute_difference": abs_diff.mean().item(),
+        "max_relative_difference": rel_diff.max().item(),
+        "mean_relative_difference": rel_diff.mean().item(),
+        "cosine_similarity": torch.nn.functional.cosine_similarity(f.flatten().unsqueeze(0),
+                                                                    ref.flatten().unsqueeze(0)).item(),
+        "atol": atol,
+        "rtol": rtol,
+        "flash_output_stats": stats(f),
+        "reference_output_stats": stats(ref),
+        "input_shape": q.shape,
+        "configuration": {
+            "causal": causal,
+            "dropout_p": dropout_p,
+            "has_bias": bias is not None,
+            "dtype": str(q.dtype),
+            "device": str(q.device),
+        },
+    }
+
+
+@contextlib.contextmanager
+def gradient_checkpointing_mode(enable: bool = True):
+    """Accepted for compatibility (reference ``ops/attention.py:721-726``, a
+    placeholder there too): the backward already recomputes P tile by tile."""
+    yield
+
+
+@contextlib.contextmanager
+def mixed_precision_mode(enable: bool = True):
+    """Autocast region on the GPU (reference ``ops/attention.py:729-736``)."""
+    if enable and torch.cuda.is_available():
+        with torch.autocast(device_type="cuda"):
+            yield
+    else:
+        yield
+
+
+flash_attention_forward = flash_attention_forward_enhanced
+flash_attention_backward = flash_attention_backward_enhanced
+compare_with_pytorch_attention = compare_with_pytorch_attention_enhanced

@@ -159,3 +159,22 @@ def test_kernel_errors_raise_not_fall_back():
         fa.flash_attention_v100(q, k, v)
     with pytest.raises(NotImplementedError):
         fa.flash_attention_v100(q, k, v, fallback_on_error=False)
+
+
+def test_standalone_forward_backward_and_compare():
+    # reference ops/attention.py:464-718: forward only, backward from saved state, report dict
+    from flash_attention_v100 import ops
+    q, k, v, do = (t.to(DEV) for t in make_inputs(2, 200, 4, 64, torch.bfloat16, Hkv=2, seed=21))
+    bias = torch.randn(1, 4, 200, 200, device=DEV).to(torch.bfloat16)
+    o = ops.flash_attention_forward(q, k, v, None, True, 0.0, bias)
+    o2, lse, mx = fa.flash_attention_forward_triton_enhanced(q, k, v, 64 ** -0.5, True, bias=bias)
+    assert torch.equal(o, o2)
+    dq, dk, dv = ops.flash_attention_backward(do, q, k, v, o2, lse, mx, 64 ** -0.5, True, bias=bias)
+    dq2, dk2, dv2 = _lib.bwd(q, k, v, o2, do, lse, True, 64 ** -0.5, bias=bias)
+    assert torch.equal(dq, dq2) and torch.equal(dk, dk2) and torch.equal(dv, dv2)
+    for p, causal, b in ((0.0, True, bias), (0.1, False, None)):
+        r = ops.compare_with_pytorch_attention(q, k, v, causal, b, p, atol=2e-2, rtol=2e-2)
+        say(f"compare p={p} causal={causal}: max abs {r['max_absolute_difference']:.3e} "
+            f"cos {r['cosine_similarity']:.6f}")
+        assert r["allclose"] and r["cosine_similarity"] > 0.9999
+        assert r["configuration"]["has_bias"] == (b is not None) and r["input_shape"] == q.shape

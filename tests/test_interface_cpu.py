@@ -51,6 +51,32 @@ def test_kernel_launcher_signatures():
                             "block_size_n", "enable_fused_delta", "enable_gradient_accumulation", "use_fast_math"]
 
 
+def test_standalone_function_signatures_and_aliases():
+    # reference ops/attention.py:464-475, 539-550, 603-612 and the aliases at :756-759
+    from flash_attention_v100 import ops
+    f = inspect.signature(ops.flash_attention_forward_enhanced).parameters
+    assert list(f)[:9] == ["q", "k", "v", "scale", "causal", "dropout_p", "bias", "enable_multi_gpu",
+                           "performance_mode"]
+    b = inspect.signature(ops.flash_attention_backward_enhanced).parameters
+    assert list(b)[:10] == ["grad_output", "q", "k", "v", "output", "lse", "max_vals", "scale", "causal",
+                            "enable_multi_gpu"]
+    c = inspect.signature(ops.compare_with_pytorch_attention_enhanced).parameters
+    assert [(n, p.default) for n, p in list(c.items())[3:]] == [
+        ("causal", False), ("bias", None), ("dropout_p", 0.0), ("atol", 1e-4), ("rtol", 1e-4)]
+    assert ops.flash_attention_forward is ops.flash_attention_forward_enhanced is fa.flash_attention_forward
+    assert ops.flash_attention_backward is ops.flash_attention_backward_enhanced is fa.flash_attention_backward
+    assert ops.compare_with_pytorch_attention is ops.compare_with_pytorch_attention_enhanced
+    with ops.gradient_checkpointing_mode(), ops.mixed_precision_mode(False):
+        pass
+
+
+def test_standalone_functions_reject_cpu_tensors():
+    from flash_attention_v100 import ops
+    q = torch.zeros(1, 8, 2, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="GPU"):
+        ops.flash_attention_forward(q, q, q)
+
+
 def _t(*shape, dtype=torch.float16):
     return torch.zeros(*shape, dtype=dtype)
 
