@@ -204,3 +204,32 @@ def test_bias_deterministic():
     b = run_kernels(q, k, v, do, True, 0.1, bias)
     for x, y in zip(a, b):
         assert torch.equal(x, y)
+
+
+def test_bias_views():
+    # expanded (stride-0) views, a slice of a wider row buffer, and a transposed
+    # (non-unit key stride) view all give the result of the materialised bias
+    B, S, H, D = 2, 96, 2, 64
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, S, H, D, torch.bfloat16, seed=18))
+    base = make_bias((1, 1, S, S), torch.bfloat16).to(DEV)
+    wide = torch.zeros(B, H, S, S + 40, device=DEV, dtype=torch.bfloat16)
+    wide[..., 8:8 + S] = base
+    views = {
+        "expanded": base.expand(B, H, S, S),
+        "sliced": wide[..., 8:8 + S],
+        "transposed": base.expand(B, H, S, S).transpose(-1, -2).contiguous().transpose(-1, -2),
+    }
+    ref = fa.flash_attention_v100(q, k, v, causal=True, bias=base.expand(B, H, S, S).contiguous())
+    for name, bv in views.items():
+        say(f"case: bias view {name} strides {bv.stride()}")
+        out = fa.flash_attention_v100(q, k, v, causal=True, bias=bv)
+        assert torch.equal(out, ref), name
+    # gradients through an expanded view land on the (1, 1, S, S) leaf
+    leaf = base.clone().requires_grad_(True)
+    o = fa.flash_attention_v100(q, k, v, causal=True, bias=leaf.expand(B, H, S, S))
+    o.backward(do)
+    _, lse, _ = _lib.fwd(q, k, v, True, D ** -0.5, bias=base.expand(B, H, S, S).contiguous())
+    *_, db = _lib.bwd(q, k, v, o.detach(), do, lse, True, D ** -0.5,
+                      bias=base.expand(B, H, S, S).contiguous(), want_dbias=True)
+    assert leaf.grad.shape == (1, 1, S, S)
+    assert torch.allclose(leaf.grad.float(), db.float().sum((0, 1), keepdim=True), atol=2e-2, rtol=2e-2)
