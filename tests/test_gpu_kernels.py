@@ -201,3 +201,37 @@ def test_empty_keys():
     o, lse, _ = _lib.fwd(q, k, k, False, 0.125)
     torch.cuda.synchronize()
     assert torch.equal(o, torch.zeros_like(o)) and bool((lse == float("-inf")).all())
+
+
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_bwd_stages_on_two_streams(with_bias):
+    # include/fa_abi.h: after stage 0, stages 1 (dK/dV [+ dBias]) and 2 (dQ) are
+    # independent and may run on two streams; results equal fa_bwd's bit for bit
+    import ctypes
+    say(f"case: fa_bwd_stage on two streams, bias={with_bias}")
+    B, S, H, D = 2, 333, 4, 64
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, S, H, D, torch.bfloat16, Hkv=2, seed=31))
+    pb = None
+    if with_bias:
+        bias = torch.randn(1, H, S, S, device=DEV).to(torch.bfloat16)
+        pb = _lib.prepare_bias(bias, B, H, S, S, torch.bfloat16)
+    o, lse, _ = _lib.fwd(q, k, v, True, D ** -0.5, bias=pb)
+    ref = _lib.bwd(q, k, v, o, do, lse, True, D ** -0.5, bias=pb, want_dbias=with_bias)
+    lib = _lib.load()
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    db = torch.empty(1, H, S, 336, device=DEV)[..., :S] if with_bias else None
+    a = _lib.bwd_args(q, k, v, o, do, lse, dq, dk, dv, True, D ** -0.5, 0.0, 0, 0, pb, db)
+    ws = torch.empty(lib.fa_bwd_workspace_size(ctypes.byref(a)), device=DEV, dtype=torch.uint8)
+    wsp = ctypes.c_void_p(ws.data_ptr())
+    s0, s1, s2 = torch.cuda.current_stream(), torch.cuda.Stream(), torch.cuda.Stream()
+    assert lib.fa_bwd_stage(ctypes.byref(a), wsp, ws.numel(), 0, ctypes.c_void_p(s0.cuda_stream)) == 0
+    s1.wait_stream(s0)
+    s2.wait_stream(s0)
+    assert lib.fa_bwd_stage(ctypes.byref(a), wsp, ws.numel(), 1, ctypes.c_void_p(s1.cuda_stream)) == 0
+    assert lib.fa_bwd_stage(ctypes.byref(a), wsp, ws.numel(), 2, ctypes.c_void_p(s2.cuda_stream)) == 0
+    s0.wait_stream(s1)
+    s0.wait_stream(s2)
+    torch.cuda.synchronize()
+    assert torch.equal(dq, ref[0]) and torch.equal(dk, ref[1]) and torch.equal(dv, ref[2])
+    if with_bias:
+        assert torch.equal(db.to(torch.bfloat16), ref[3])
