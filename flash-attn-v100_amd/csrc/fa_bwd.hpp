@@ -218,13 +218,14 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
     // one per-lane offset (key, row parity); the query rows go in the scalar
     // offset.  Rows past Sq read zeros (P = 0 there anyway); lanes past Sk read
     // zeros or another row and are never stored.
-    // 16-bit values are kept two to a register (rows r, r + 1)
+    // 16-bit values are kept two to a register (rows r, r + 1).  The values of
+    // the next sub-step are loaded while the current one computes (bnext).
     constexpr bool B16 = BIAS && !Elem<BT>::kF32;
     constexpr int NBI = BIAS ? (B16 ? 8 : 16) : 1;
     using BR = typename std::conditional<B16, s16x2, float>::type;
-    BR braw[NBI];
+    BR braw[NBI], bnext[NBI];
     const int bvoff = (4 * hi * (int)p.bias_ss + kj) * (int)sizeof(BT);
-    auto load_bias = [&](int it, int st) FA_INLINE {
+    auto load_bias = [&](BR (&dst)[NBI], int it, int st) FA_INLINE {
         if constexpr (BIAS) {
             const __amdgpu_buffer_rsrc_t rs =
                 slice_buffer((const BT*)p.bias + b * p.bias_sb + tile_head(it) * p.bias_sh, p.bias_span);
@@ -233,9 +234,9 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
             for (int r = 0; r < 16; ++r) {
                 const auto x = load_bias1<BT>(rs, bvoff, (qb0 + 8 * (r >> 2) + (r & 3)) * (int)p.bias_ss * (int)sizeof(BT));
                 if constexpr (B16)
-                    braw[r >> 1][r & 1] = x;
+                    dst[r >> 1][r & 1] = x;
                 else
-                    braw[r] = x;
+                    dst[r] = x;
             }
         }
     };
@@ -347,7 +348,10 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
     // interleaves the MFMA, softmax and LDS phases of two waves.
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    if (total > 0) issue(0, 0);
+    if (total > 0) {
+        issue(0, 0);
+        load_bias(bnext, 0, 0);
+    }
     f32x16 sc, dpc;
     int bcur = 0;  // it & 1
     auto iter = [&](int it, auto mask_tag) FA_INLINE {
@@ -355,7 +359,14 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
         issue(min(it + 1, total - 1), bcur ^ 1);
 #pragma unroll
         for (int st = 0; st < C::NSUB; ++st) {
-            load_bias(it, st);
+            if constexpr (BIAS) {  // this sub-step's bias; start loading the next one's
+#pragma unroll
+                for (int r = 0; r < NBI; ++r) braw[r] = bnext[r];
+                if (st + 1 < C::NSUB)
+                    load_bias(bnext, it, st + 1);
+                else
+                    load_bias(bnext, min(it + 1, total - 1), 0);
+            }
             sdp(bcur, st, sc, dpc);
             softmax_ds(it, bcur, st, sc, dpc, mask_tag);
             dkdv_acc(bcur, st, I0{});
