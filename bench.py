@@ -14,9 +14,9 @@ same workload) ride along.
 
 With ``--bias full`` (a (B, H, S, S) bf16 additive bias) or ``--bias heads``
 (a (1, H, S, S) one, shared over the batch) the same step runs the bias path of
-the kernels; ``--dbias`` also produces the bias gradient (the fp32 dS written by
-the dK/dV kernel; for ``heads`` its sum over the batch, done by the library),
-inside the timed step.
+the kernels; ``--dbias`` also produces the bias gradient in the bias dtype (dS
+from the dK/dV kernel, accumulated in fp32; for ``heads`` its sum over the batch,
+done by the library), inside the timed step.
 The FLOP count is the same (the bias adds no matrix products).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
@@ -67,8 +67,8 @@ def gpu_bench(steps: int, warmup: int, bias_kind: str = "none", want_dbias: bool
     if bias_kind != "none":
         bias = torch.randn(BIAS_SHAPES[bias_kind], device="cuda", dtype=torch.float32).to(torch.bfloat16)
         pb = _lib.prepare_bias(bias, B, H, S, S, torch.bfloat16)
-        if want_dbias:  # (1, H, S, S) for the shared bias: the library sums over the batch
-            dbias = torch.empty(BIAS_SHAPES[bias_kind], device="cuda", dtype=torch.float32)
+        if want_dbias:  # bias dtype; (1, H, S, S) for the shared bias: the library sums over the batch
+            dbias = torch.empty(BIAS_SHAPES[bias_kind], device="cuda", dtype=torch.bfloat16)
     fa = _lib.fwd_args(q, k, v, o, lse, None, CAUSAL, scale, 0.0, 0, 0, pb)
     ba = _lib.bwd_args(q, k, v, o, do, lse, dq, dk, dv, CAUSAL, scale, 0.0, 0, 0, pb, dbias)
     ws_bytes = lib.fa_bwd_workspace_size(ctypes.byref(ba))

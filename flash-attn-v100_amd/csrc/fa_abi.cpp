@@ -99,15 +99,18 @@ bool dbias_reduced(const fa_bwd_args* a) {
 // key row length of the parts: Sk rounded up to 4 (16-byte rows)
 int32_t dbias_part_row(int32_t Sk) { return (Sk + 3) / 4 * 4; }
 
-// Optional bias gradient (float32): j stride 1, i stride >= Sk (rows do not
-// overlap: stores past the last row must leave the slice), 4-byte aligned
-// base, non-negative strides.  Summed form: 16-byte aligned base and strides
-// that are multiples of 4 (16-byte stores of 4 keys).
+// Optional bias gradient: dtype fp16, bf16 or fp32; j stride 1, i stride >= Sk
+// (rows do not overlap: stores past the last row must leave the slice),
+// element-aligned base, non-negative strides.  Summed form: 16-byte aligned
+// base and strides that are multiples of 4 (one store of 4 keys).
 int32_t check_dbias(const fa_bwd_args* a) {
-    const float* dbias = a->dbias;
+    const void* dbias = a->dbias;
     const int64_t* st = a->dbias_stride;
     if (!dbias) return FA_OK;
-    if (((uintptr_t)dbias & 3u) || st[3] != 1 || st[2] < a->seqlen_k) return FA_ERR_BIAS;
+    const int32_t dt = a->dbias_dtype;
+    if (dt != FA_DTYPE_F16 && dt != FA_DTYPE_BF16 && dt != FA_DTYPE_F32) return FA_ERR_BIAS;
+    const int es = elem_size(dt);
+    if (((uintptr_t)dbias % (uintptr_t)es) || st[3] != 1 || st[2] < a->seqlen_k) return FA_ERR_BIAS;
     for (int i = 0; i < 3; ++i)
         if (st[i] < 0) return FA_ERR_BIAS;
     if (dbias_reduced(a)) {
@@ -117,7 +120,7 @@ int32_t check_dbias(const fa_bwd_args* a) {
         const int64_t part_st[4] = {0, 0, dbias_part_row(a->seqlen_k), 1};
         if (check_slice_offsets(part_st, a->seqlen_q, a->seqlen_k, 4)) return FA_ERR_TOO_LARGE;
     }
-    return check_slice_offsets(st, a->seqlen_q, a->seqlen_k, 4);
+    return check_slice_offsets(st, a->seqlen_q, a->seqlen_k, es);
 }
 
 // Backward workspace: B * H rows of 2 * sq_pad float32 (LSE * log2 e, then
@@ -161,7 +164,8 @@ const char* fa_strerror(int32_t code) {
         case FA_ERR_TOO_LARGE: return "problem too large for the kernel grid";
         case FA_ERR_BIAS:
             return "bias needs the input dtype or float32, j stride 1, b/h/i strides multiples of 16 bytes and a "
-                   "16-byte aligned base; dbias needs a bias, j stride 1 and a 4-byte aligned base";
+                   "16-byte aligned base; dbias needs a bias, dtype fp16/bf16/fp32, j stride 1, i stride >= Sk "
+                   "and an aligned base";
         default: return "unknown status code";
     }
 }
@@ -336,14 +340,17 @@ int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int
     if (reduce_db) {  // parts in the workspace, summed into dbias after dK/dV
         const int SkP = dbias_part_row(a->seqlen_k);
         const int64_t part_st[4] = {(int64_t)a->num_heads * a->seqlen_q * SkP, (int64_t)a->seqlen_q * SkP, SkP, 1};
-        p.dbias = (float*)((char*)workspace + ws_rows_bytes(a));
+        p.dbias = (char*)workspace + ws_rows_bytes(a);
         p.dbias_sb = part_st[0];
         p.dbias_sh = part_st[1];
         p.dbias_ss = part_st[2];
         p.dbias_span = slice_span(part_st, a->seqlen_q, a->seqlen_k, 4);
+        p.dbias_dtype = FA_DTYPE_F32;
+        p.dbias_es = 4;
         p.dbias_zero_fill = 0;
-        rp.part = p.dbias;
+        rp.part = (const float*)p.dbias;
         rp.out = a->dbias;
+        rp.out_dtype = a->dbias_dtype;
         rp.out_sb = a->dbias_stride[0];
         rp.out_sh = a->dbias_stride[1];
         rp.out_ss = a->dbias_stride[2];
@@ -360,7 +367,9 @@ int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int
         p.dbias_sb = a->dbias_stride[0];
         p.dbias_sh = a->dbias_stride[1];
         p.dbias_ss = a->dbias_stride[2];
-        p.dbias_span = a->dbias ? slice_span(a->dbias_stride, a->seqlen_q, a->seqlen_k, 4) : 0;
+        p.dbias_es = a->dbias ? elem_size(a->dbias_dtype) : 4;
+        p.dbias_dtype = a->dbias ? a->dbias_dtype : FA_DTYPE_F32;
+        p.dbias_span = a->dbias ? slice_span(a->dbias_stride, a->seqlen_q, a->seqlen_k, p.dbias_es) : 0;
         p.dbias_zero_fill = 1;
     }
     const bool causal = a->causal != 0;

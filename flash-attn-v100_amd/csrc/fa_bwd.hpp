@@ -248,9 +248,9 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
     };
     // dBias stores: lanes past Sk are sent out of range; rows past Sq land past
     // the slice (query stride >= Sk) and are dropped
-    const int dbvoff = kj < p.Sk ? (4 * hi * (int)p.dbias_ss + kj) * 4 : kOffNowhere;
+    const int dbvoff = kj < p.Sk ? (4 * hi * (int)p.dbias_ss + kj) * p.dbias_es : kOffNowhere;
     auto dbias_buf = [&](int hh) FA_INLINE {
-        return slice_buffer(p.dbias + b * p.dbias_sb + hh * p.dbias_sh, p.dbias_span);
+        return slice_buffer((const char*)p.dbias + (b * p.dbias_sb + hh * p.dbias_sh) * p.dbias_es, p.dbias_span);
     };
 
     // ---- P and dS of tile `it` (buffer s); dS = P (dP - delta), scale applied at the end ----
@@ -294,9 +294,12 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
             }
         }
         if (want_db) {
+            with_grad_dtype(p.dbias_dtype, [&](auto dt) FA_INLINE {
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                store_f32(dbrs, ds[r], dbvoff, (qb0 + 8 * (r >> 2) + (r & 3)) * (int)p.dbias_ss * 4);
+                for (int r = 0; r < 16; ++r)
+                    store_grad<decltype(dt)::value>(dbrs, ds[r], dbvoff,
+                                                    (qb0 + 8 * (r >> 2) + (r & 3)) * (int)p.dbias_ss * p.dbias_es);
+            });
         }
         if constexpr (!C::F32) {
 #pragma unroll
@@ -380,8 +383,11 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
         const int zrows = min(qt_begin * BQ, p.Sq);
         for (int g = 0; g < p.group; ++g) {
             const __amdgpu_buffer_rsrc_t rs = dbias_buf(hk * p.group + g);
-            const int voff = kj < p.Sk ? (hi * (int)p.dbias_ss + kj) * 4 : kOffNowhere;
-            for (int q = 0; q < zrows; q += 2) store_f32(rs, 0.f, voff, q * (int)p.dbias_ss * 4);
+            const int voff = kj < p.Sk ? (hi * (int)p.dbias_ss + kj) * p.dbias_es : kOffNowhere;
+            with_grad_dtype(p.dbias_dtype, [&](auto dt) FA_INLINE {
+                for (int q = 0; q < zrows; q += 2)
+                    store_grad<decltype(dt)::value>(rs, 0.f, voff, q * (int)p.dbias_ss * p.dbias_es);
+            });
         }
     }
 

@@ -157,9 +157,27 @@ __device__ FA_INLINE inline bias1_t<T> load_bias1(__amdgpu_buffer_rsrc_t rs, int
         return (short)__builtin_amdgcn_raw_buffer_load_b16(rs, voff, soff, 0);
 }
 
-// one float32 store at byte offset voff + soff (dropped past the range)
-__device__ FA_INLINE inline void store_f32(__amdgpu_buffer_rsrc_t rs, float x, int voff, int soff) {
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, x), rs, voff, soff, 0);
+// one gradient element at byte offset voff + soff (dropped past the range),
+// rounded to DT (0 fp16, 1 bf16, 2 fp32)
+template <int DT>
+__device__ FA_INLINE inline void store_grad(__amdgpu_buffer_rsrc_t rs, float x, int voff, int soff) {
+    if constexpr (DT == 2)
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, x), rs, voff, soff, 0);
+    else if constexpr (DT == 1)
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (bf16)x), rs, voff, soff, 0);
+    else
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (f16)x), rs, voff, soff, 0);
+}
+// f(std::integral_constant<int, DT>) for the wave-uniform runtime dtype code,
+// so that a block of stores branches once
+template <typename F>
+__device__ FA_INLINE inline void with_grad_dtype(int dtype, F&& f) {
+    if (dtype == 2)
+        f(std::integral_constant<int, 2>{});
+    else if (dtype == 1)
+        f(std::integral_constant<int, 1>{});
+    else
+        f(std::integral_constant<int, 0>{});
 }
 // a lane offset that lands every access of the lane out of range (offsets
 // past it stay below 2^32, so they cannot wrap back into the range)

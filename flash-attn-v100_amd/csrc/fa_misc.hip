@@ -61,12 +61,25 @@ __global__ __launch_bounds__(256) void dbias_reduce_kernel(const DbiasReducePara
             if (j + 3 > i) acc.w = 0.f;
         }
     }
-    float* o = r.out + bo * r.out_sb + ho * r.out_sh + (int64_t)i * r.out_ss + j;
-    if (j + 4 <= r.Sk) {
-        *reinterpret_cast<float4*>(o) = acc;
+    const int64_t oe = bo * r.out_sb + ho * r.out_sh + (int64_t)i * r.out_ss + j;  // element index
+    const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+    const int n_out = min(4, r.Sk - j);
+    if (r.out_dtype == 2) {
+        float* o = (float*)r.out + oe;
+        if (n_out == 4)
+            *reinterpret_cast<float4*>(o) = acc;
+        else
+            for (int e = 0; e < n_out; ++e) o[e] = a[e];
     } else {
-        const float a[4] = {acc.x, acc.y, acc.z, acc.w};
-        for (int e = 0; e < r.Sk - j; ++e) o[e] = a[e];
+        unsigned short h[4];
+        for (int e = 0; e < 4; ++e)
+            h[e] = r.out_dtype == 1 ? __builtin_bit_cast(unsigned short, (bf16)a[e])
+                                    : __builtin_bit_cast(unsigned short, (f16)a[e]);
+        unsigned short* o = (unsigned short*)r.out + oe;
+        if (n_out == 4)
+            *reinterpret_cast<uint2*>(o) = make_uint2(h[0] | (unsigned)h[1] << 16, h[2] | (unsigned)h[3] << 16);
+        else
+            for (int e = 0; e < n_out; ++e) o[e] = h[e];
     }
 }
 

@@ -63,9 +63,11 @@ struct BwdParams {
     const void* bias;  // as in FwdParams
     int64_t bias_sb, bias_sh, bias_ss;
     int bias_span;
-    float* dbias;      // optional fp32 (B, H, Sq, Sk) gradient of the bias, key stride 1
+    void* dbias;       // optional (B, H, Sq, Sk) gradient of the bias, key stride 1
     int64_t dbias_sb, dbias_sh, dbias_ss;  // query stride >= Sk
     int dbias_span;    // bytes of one (batch, head) slice
+    int dbias_dtype;   // 0 fp16, 1 bf16, 2 fp32 (the FA_DTYPE_* codes)
+    int dbias_es;      // its element size in bytes
     int dbias_zero_fill;  // causal: also zero the rows of query tiles the loop skips
 };
 
@@ -76,7 +78,8 @@ struct BwdParams {
 // leaves the parts of skipped query tiles unwritten).
 struct DbiasReduceParams {
     const float* part;
-    float* out;
+    void* out;
+    int out_dtype;  // 0 fp16, 1 bf16, 2 fp32
     int64_t out_sb, out_sh, out_ss;
     int B, H, Sq, Sk, SkP;
     int sum_b, sum_h, causal;

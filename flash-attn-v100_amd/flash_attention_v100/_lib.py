@@ -65,7 +65,7 @@ class BwdArgs(ctypes.Structure):
         ("scale", ctypes.c_float), ("dropout_p", ctypes.c_float),
         ("seed", ctypes.c_uint64), ("offset", ctypes.c_uint64),
         ("bias", ctypes.c_void_p), ("bias_stride", _I64x4), ("bias_dtype", ctypes.c_int32),
-        ("dbias", ctypes.c_void_p), ("dbias_stride", _I64x4),
+        ("dbias", ctypes.c_void_p), ("dbias_stride", _I64x4), ("dbias_dtype", ctypes.c_int32),
     ]
 
 
@@ -204,8 +204,8 @@ def prepare_bias(bias: torch.Tensor, B: int, H: int, Sq: int, Sk: int, dtype: to
 
 
 def reduce_dbias(dbias: torch.Tensor, pb: PreparedBias) -> torch.Tensor:
-    """Sum the (B, H, Sq, Sk) float32 score gradient over the dimensions the
-    caller's bias broadcast and cast it to the bias's dtype."""
+    """Sum the score gradient over the dimensions of the caller's bias that are
+    still broadcast (size 1 there, not here) and cast it to the bias's dtype."""
     dims = [d for d in range(4) if pb.shape[d] == 1 and dbias.shape[d] != 1]
     g = dbias.sum(dim=dims, keepdim=True) if dims else dbias
     return g.to(pb.dtype)
@@ -260,7 +260,8 @@ def bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, of
         bias.strides if bias is not None else _I64x4(0, 0, 0, 1),
         bias.dtype_code if bias is not None else DTYPE_CODES[q.dtype],
         dbias.data_ptr() if dbias is not None else None,
-        _dbias_strides(dbias) if dbias is not None else _I64x4(0, 0, 0, 1))
+        _dbias_strides(dbias) if dbias is not None else _I64x4(0, 0, 0, 1),
+        DTYPE_CODES[dbias.dtype] if dbias is not None else DTYPE_CODES[torch.float32])
 
 
 def _dbias_strides(dbias):
@@ -288,13 +289,15 @@ def bwd(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float = 0.0,
         Sk = k.shape[1]
         # batch / head dimensions the bias broadcasts are summed by the library;
         # every element is written (zeros where causal masks).  Summed rows are
-        # 16-byte aligned (padded to 4 keys).
+        # 16-byte aligned (padded to 4 keys).  The library writes the caller's
+        # dtype directly unless a query-dimension sum is left to do here (in fp32).
         Bo = 1 if pb.shape[0] == 1 else B
         Ho = 1 if pb.shape[1] == 1 else H
+        gdt = pb.dtype if (pb.dtype in DTYPE_CODES and (pb.shape[2] != 1 or Sq == 1)) else torch.float32
         if (Bo, Ho) == (B, H):
-            dbias = torch.empty((B, H, Sq, Sk), device=q.device, dtype=torch.float32)
+            dbias = torch.empty((B, H, Sq, Sk), device=q.device, dtype=gdt)
         else:
-            dbias = torch.empty((Bo, Ho, Sq, -(-Sk // 4) * 4), device=q.device, dtype=torch.float32)[..., :Sk]
+            dbias = torch.empty((Bo, Ho, Sq, -(-Sk // 4) * 4), device=q.device, dtype=gdt)[..., :Sk]
     a = bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, offset, pb, dbias)
     ws_bytes = lib.fa_bwd_workspace_size(ctypes.byref(a))
     ws = torch.empty(max(int(ws_bytes), 256), device=q.device, dtype=torch.uint8)

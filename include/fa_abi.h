@@ -103,12 +103,13 @@ typedef struct fa_fwd_args {
  * (the reference dropped them, ops/attention.py:209-227) and writes dq, dk,
  * dv in the input dtype (fully overwritten, no zero-init needed).  With a
  * bias, the forward's bias is passed again; if dbias is non-NULL the kernels
- * also write dS = d loss / d(scaled score + bias) into it, float32, logically
- * (B, H, Sq, Sk) with its own (b, h, i, j) strides (the reference returned
+ * also write dS = d loss / d(scaled score + bias) into it, logically
+ * (B, H, Sq, Sk) with its own (b, h, i, j) strides, as element type
+ * dbias_dtype (computed in float32, rounded once) (the reference returned
  * zeros, ops/attention.py:297-301).  A zero b or h stride of dbias sums the
  * gradient over that dimension (the gradient of a bias broadcast over it):
- * the workspace then also holds the per-(b, h) parts, and dbias needs a
- * 16-byte aligned base and strides that are multiples of 4. */
+ * the workspace then also holds the float32 per-(b, h) parts, and dbias needs
+ * a 16-byte aligned base and strides that are multiples of 4. */
 typedef struct fa_bwd_args {
     const void* q;
     const void* k;
@@ -142,8 +143,9 @@ typedef struct fa_bwd_args {
     const void* bias;         /* optional, as in fa_fwd_args */
     int64_t bias_stride[4];
     int32_t bias_dtype;
-    float* dbias;             /* optional float32 (B, H, Sq, Sk) gradient of the bias, fully written */
+    void* dbias;              /* optional (B, H, Sq, Sk) gradient of the bias, fully written */
     int64_t dbias_stride[4];  /* (b, h, i, j) in elements; j stride 1, i stride >= Sk; b, h: 0 = sum */
+    int32_t dbias_dtype;      /* FA_DTYPE_* of dbias */
 } fa_bwd_args;
 
 /* Library ABI version (FA_ABI_VERSION).  No reference counterpart. */

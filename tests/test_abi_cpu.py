@@ -63,7 +63,7 @@ int main(void) {
   F(fa_bwd_args, dout) F(fa_bwd_args, lse) F(fa_bwd_args, dv) F(fa_bwd_args, do_stride)
   F(fa_bwd_args, dv_stride) F(fa_bwd_args, batch) F(fa_bwd_args, causal) F(fa_bwd_args, scale)
   F(fa_bwd_args, seed) F(fa_bwd_args, offset) F(fa_bwd_args, bias) F(fa_bwd_args, bias_stride)
-  F(fa_bwd_args, bias_dtype) F(fa_bwd_args, dbias) F(fa_bwd_args, dbias_stride)
+  F(fa_bwd_args, bias_dtype) F(fa_bwd_args, dbias) F(fa_bwd_args, dbias_stride) F(fa_bwd_args, dbias_dtype)
   return 0;
 }
 """
@@ -244,6 +244,15 @@ def test_bwd_check_dbias_rules():
     assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_ERR_BIAS"]
     a = _lib.bwd_args(q, q, q, q, q, lse, q, q, q, True, 0.125, 0.0, 0, 0, None, db)
     assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_ERR_BIAS"]  # dbias without a bias
+    a = _lib.bwd_args(q, q, q, q, q, lse, q, q, q, True, 0.125, 0.0, 0, 0, pb, db)
+    a.dbias_dtype = 5
+    assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_ERR_BIAS"]  # unknown dtype
+    db16 = torch.zeros(B, H, S, S, dtype=torch.bfloat16)
+    a = _lib.bwd_args(q, q, q, q, q, lse, q, q, q, True, 0.125, 0.0, 0, 0, pb, db16)
+    assert a.dbias_dtype == _lib.DTYPE_CODES[torch.bfloat16]
+    assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_OK"]
+    a.dbias = a.dbias + 1  # not element-aligned
+    assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_ERR_BIAS"]
 
 
 def test_prepare_bias_layout():
