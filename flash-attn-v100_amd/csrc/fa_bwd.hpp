@@ -20,7 +20,8 @@
 // Diagonal (causal) tiles run a separate masking variant of each tile step.
 // With an additive bias (BIAS) both kernels add bias * log2 e to the scores
 // before the exponent; dkdv_kernel, the one kernel that visits every
-// (query, key) pair once, also writes dBias = dS (fp32, unscaled) when asked.
+// (query, key) pair once, also writes dBias = dS (unscaled, rounded once to the
+// requested dtype) when asked.
 // All five products accumulate in fp32 and are rounded once to the input dtype.
 #pragma once
 
