@@ -219,8 +219,11 @@ __device__ FA_INLINE inline uint32_t philox_word0(uint64_t seed, uint64_t ctr) {
     uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
 #pragma unroll
     for (int r = 0; r < 10; ++r) {
-        const uint32_t hb = __umulhi(0xCD9E8D57u, c2), lb = 0xCD9E8D57u * c2;
-        const uint32_t ha = __umulhi(0xD2511F53u, c0), la = 0xD2511F53u * c0;
+        // one 32 x 32 -> 64-bit product per multiplier (v_mad_u64_u32 gives
+        // both halves; separate mul_hi / mul_lo cost twice the multiplies)
+        const uint64_t pb = (uint64_t)0xCD9E8D57u * c2, pa = (uint64_t)0xD2511F53u * c0;
+        const uint32_t hb = (uint32_t)(pb >> 32), lb = (uint32_t)pb;
+        const uint32_t ha = (uint32_t)(pa >> 32), la = (uint32_t)pa;
         c0 = hb ^ c1 ^ k0;
         c2 = ha ^ c3 ^ k1;
         c1 = lb;
