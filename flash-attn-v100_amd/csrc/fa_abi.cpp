@@ -218,6 +218,7 @@ int32_t fa_fwd(const fa_fwd_args* a, void* stream) {
     p.scale_log2 = a->scale * 1.4426950408889634f;
     p.dropout_p = a->dropout_p;
     p.rp = 1.f / (1.f - a->dropout_p);
+    p.keep_thresh = fa::keep_threshold(a->dropout_p);
     p.seed = a->seed;
     p.offset = a->offset;
     p.bias = a->bias;
@@ -328,6 +329,7 @@ int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int
     p.scale_log2 = a->scale * 1.4426950408889634f;
     p.dropout_p = a->dropout_p;
     p.rp = 1.f / (1.f - a->dropout_p);
+    p.keep_thresh = fa::keep_threshold(a->dropout_p);
     p.seed = a->seed;
     p.offset = a->offset;
     p.bias = a->bias;

@@ -285,8 +285,7 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
                 float dpv = dpc[r];
                 float pdv = pv;
                 if (DROPOUT) {
-                    const float u = philox_uniform(p.seed, col_ctr + (uint64_t)q * (uint64_t)p.Sk);
-                    const float z = u > p.dropout_p ? p.rp : 0.f;
+                    const float z = philox_keep(p.seed, col_ctr + (uint64_t)q * (uint64_t)p.Sk, p.keep_thresh) ? p.rp : 0.f;
                     dpv *= z;
                     pdv *= z;
                 }
@@ -608,8 +607,7 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
                 if (need_mask && (key >= p.Sk || (CAUSAL && key > qi))) pv = 0.f;
                 float dpv = dp[r];
                 if (DROPOUT) {
-                    const float u = philox_uniform(p.seed, row_ctr + (uint64_t)key);
-                    dpv *= u > p.dropout_p ? p.rp : 0.f;
+                    dpv *= philox_keep(p.seed, row_ctr + (uint64_t)key, p.keep_thresh) ? p.rp : 0.f;
                 }
                 s[r] = pv * (dpv - del);
             }

@@ -234,6 +234,15 @@ __device__ FA_INLINE inline uint32_t philox_word0(uint64_t seed, uint64_t ctr) {
     return c0;
 }
 
+// Keep test of the dropout mask without the float mapping: u = fp32(fold(x)) *
+// 4.6566127342e-10 (fold(x) = x < 0 ? -x - 1 : x on the int32 view) is
+// non-decreasing in fold(x), so u > p exactly when fold(x) > T, with T the
+// largest fold value whose u is <= p (keep_threshold on the host).
+__device__ FA_INLINE inline bool philox_keep(uint64_t seed, uint64_t ctr, uint32_t thresh) {
+    const int32_t x = (int32_t)philox_word0(seed, ctr);
+    return (uint32_t)(x ^ (x >> 31)) > thresh;
+}
+
 __device__ FA_INLINE inline float philox_uniform(uint64_t seed, uint64_t ctr) {
     int32_t x = (int32_t)philox_word0(seed, ctr);
     x = x < 0 ? -x - 1 : x;

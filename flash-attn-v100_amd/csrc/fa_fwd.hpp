@@ -237,8 +237,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int key = k0 + 32 * blk + 8 * (r >> 2) + 4 * hi + (r & 3);
-                    const float u = philox_uniform(p.seed, row_ctr + (uint64_t)key);
-                    if (!(u > p.dropout_p)) s[blk][r] = 0.f;
+                    if (!philox_keep(p.seed, row_ctr + (uint64_t)key, p.keep_thresh)) s[blk][r] = 0.f;
                 }
         }
         if constexpr (!C::F32) {

@@ -25,6 +25,7 @@ struct FwdParams {
     float scale_log2;  // scale * log2(e)
     float dropout_p;
     float rp;          // 1 / (1 - dropout_p)
+    uint32_t keep_thresh;  // keep_threshold(dropout_p)
     uint64_t seed, offset;
     // optional additive bias (B, H, Sq, Sk) in the input dtype or float32; a
     // zero stride broadcasts that dimension, the key stride is 1
@@ -59,6 +60,7 @@ struct BwdParams {
     int sq_pad;     // Sq rounded up to kSqPad
     int ws_stride;  // 2 * sq_pad
     float scale, scale_log2, dropout_p, rp;
+    uint32_t keep_thresh;  // keep_threshold(dropout_p)
     uint64_t seed, offset;
     const void* bias;  // as in FwdParams
     int64_t bias_sb, bias_sh, bias_ss;
@@ -88,6 +90,11 @@ struct DbiasReduceParams {
 // per-(batch, head) rows of the backward workspace are padded to a multiple
 // of this many queries, so query tiles read whole rows without range checks
 constexpr int kSqPad = 128;
+
+// Largest fold value x in [0, 2^31) whose uniform fp32(x) * 4.6566127342e-10
+// (round to nearest, as the device computes it) is <= p: a mask element is
+// kept exactly when its fold value exceeds it (host code, fa_misc.hip).
+uint32_t keep_threshold(float p);
 
 // dtype-specific launchers: fa_kernels_{bf16,f16,f32}.hip without a bias,
 // fa_bias_{bf16,f16,f32}.hip with a bias of the input dtype,
