@@ -190,6 +190,7 @@ int32_t fa_fwd_check(const fa_fwd_args* a) {
         (st = check_span(a->v_stride, a->seqlen_k, a->head_dim, es)) ||
         (st = check_span(a->o_stride, a->seqlen_q, a->head_dim, es)))
         return st;
+    if ((uintptr_t)a->keep_bits & 3u) return FA_ERR_ALIGN;
     return check_bias(a->bias, a->bias_stride, a->bias_dtype, a->dtype, a->seqlen_q, a->seqlen_k);
 }
 
@@ -219,6 +220,8 @@ int32_t fa_fwd(const fa_fwd_args* a, void* stream) {
     p.dropout_p = a->dropout_p;
     p.rp = 1.f / (1.f - a->dropout_p);
     p.keep_thresh = fa::keep_threshold(a->dropout_p);
+    p.kb = a->dropout_p > 0.f ? a->keep_bits : nullptr;
+    p.kb_w = (a->seqlen_k + 31) / 32;
     p.seed = a->seed;
     p.offset = a->offset;
     p.bias = a->bias;
@@ -280,6 +283,7 @@ int32_t fa_bwd_check(const fa_bwd_args* a, size_t ws_bytes) {
     for (int i = 0; i < 8; ++i)
         if ((st = check_span(strides[i], rows[i], a->head_dim, es))) return st;
     if (a->dbias && !a->bias) return FA_ERR_BIAS;
+    if ((uintptr_t)a->keep_bits & 3u) return FA_ERR_ALIGN;
     if ((st = check_bias(a->bias, a->bias_stride, a->bias_dtype, a->dtype, a->seqlen_q, a->seqlen_k)) ||
         (st = check_dbias(a)))
         return st;
@@ -330,6 +334,8 @@ int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int
     p.dropout_p = a->dropout_p;
     p.rp = 1.f / (1.f - a->dropout_p);
     p.keep_thresh = fa::keep_threshold(a->dropout_p);
+    p.kb = a->dropout_p > 0.f ? a->keep_bits : nullptr;
+    p.kb_w = (a->seqlen_k + 31) / 32;
     p.seed = a->seed;
     p.offset = a->offset;
     p.bias = a->bias;

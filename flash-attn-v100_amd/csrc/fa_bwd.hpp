@@ -105,7 +105,7 @@ struct DkdvCfg {
 };
 
 // TB: element type of the additive bias (T or float), void = no bias
-template <typename T, int D, bool CAUSAL, bool DROPOUT, typename TB>
+template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
 __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_kernel(const BwdParams p, const int n_ktiles) {
     using C = DkdvCfg<T, D>;
     constexpr bool BIAS = !std::is_void<TB>::value;
@@ -258,16 +258,21 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
     constexpr int NPK = C::F32 ? 1 : 2;
     float pd[16], ds[16];
     s16x8 bp8[NPK], bs8[NPK];
-    auto softmax_ds = [&](int it, int s, int st, const f32x16& sc, const f32x16& dpc, auto mask_tag) FA_INLINE {
+    auto softmax_ds = [&](int it, int s, int st, const f32x16& sc, const f32x16& dpc, uint32_t kword,
+                          auto mask_tag) FA_INLINE {
         constexpr bool MASK = decltype(mask_tag)::value;
         const float* lse2 = (const float*)(buf(s) + 2 * C::QALLOC) + 32 * st;
         const float* dels = lse2 + BQ;
         const int qb0 = tile_q0(it) + 32 * st;
         const bool want_db = BIAS && p.dbias != nullptr;
         const __amdgpu_buffer_rsrc_t dbrs = dbias_buf(tile_head(it));
+        // dropout keep of query q: the Philox stream regenerated (mode 1), or
+        // the forward's words of queries qb0 + l32 transposed to this lane's
+        // key, query qb0 + 8 g + 4 hi + e at bit 8 g + e after the shift (mode 2)
         uint64_t col_ctr = 0;
-        if (DROPOUT)
+        if (DROPOUT == 1)
             col_ctr = p.offset + (uint64_t)(b * p.H + tile_head(it)) * (uint64_t)p.Sq * (uint64_t)p.Sk + (uint64_t)kj;
+        const uint32_t km = DROPOUT == 2 ? transpose32(kword, lane) >> (4 * hi) : 0u;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse2 + 8 * g + 4 * hi);
@@ -285,7 +290,10 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
                 float dpv = dpc[r];
                 float pdv = pv;
                 if (DROPOUT) {
-                    const float z = philox_keep(p.seed, col_ctr + (uint64_t)q * (uint64_t)p.Sk, p.keep_thresh) ? p.rp : 0.f;
+                    const bool keep = DROPOUT == 2 ? ((km >> (8 * g + e)) & 1u) != 0u
+                                                   : philox_keep(p.seed, col_ctr + (uint64_t)q * (uint64_t)p.Sk,
+                                                                 p.keep_thresh);
+                    const float z = keep ? p.rp : 0.f;
                     dpv *= z;
                     pdv *= z;
                 }
@@ -351,9 +359,17 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
     // interleaves the MFMA, softmax and LDS phases of two waves.
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
+    // the forward's keep word of query qb0 + l32 for the wave's 32 keys
+    auto load_kbits = [&](int it, int st) FA_INLINE -> uint32_t {
+        const int q = tile_q0(it) + 32 * st + l32;
+        if (DROPOUT != 2 || q >= p.Sq || kw0 >= p.Sk) return 0u;
+        return p.kb[((int64_t)(b * p.H + tile_head(it)) * p.Sq + q) * p.kb_w + (kw0 >> 5)];
+    };
+    uint32_t kbnext = 0;
     if (total > 0) {
         issue(0, 0);
         load_bias(bnext, 0, 0);
+        kbnext = load_kbits(0, 0);
     }
     f32x16 sc, dpc;
     int bcur = 0;  // it & 1
@@ -370,8 +386,13 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
                 else
                     load_bias(bnext, min(it + 1, total - 1), 0);
             }
+            uint32_t kbits = 0;
+            if (DROPOUT == 2) {  // likewise the keep bits
+                kbits = kbnext;
+                kbnext = st + 1 < C::NSUB ? load_kbits(it, st + 1) : load_kbits(min(it + 1, total - 1), 0);
+            }
             sdp(bcur, st, sc, dpc);
-            softmax_ds(it, bcur, st, sc, dpc, mask_tag);
+            softmax_ds(it, bcur, st, sc, dpc, kbits, mask_tag);
             dkdv_acc(bcur, st, I0{});
             dkdv_acc(bcur, st, I1{});
         }
@@ -465,7 +486,7 @@ struct DqCfg {
     static constexpr int MIN_BLOCKS = (F32 && D == 128) ? 1 : 2;
 };
 
-template <typename T, int D, bool CAUSAL, bool DROPOUT, typename TB>
+template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
 __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(const BwdParams p, const int n_qtiles) {
     using C = DqCfg<T, D>;
     constexpr bool BIAS = !std::is_void<TB>::value;
@@ -568,6 +589,10 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
                 else
                     load_all(std::false_type{});
             }
+            // the forward's keep bits of this lane's query for the sub-step's keys
+            uint32_t kword = 0;
+            if (DROPOUT == 2 && qi < p.Sq)
+                kword = p.kb[((int64_t)(b * p.H + h) * p.Sq + qi) * p.kb_w + (k0 >> 5)];
             // ---- S^T = K Q^T, dP^T = V dO^T (C[key][query]) ----
             f32x16 s = f32x16{}, dp = f32x16{};
             const T* krow = Ks + l32 * KW;
@@ -596,6 +621,8 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
             }
             // ---- dS^T = P^T (dP^T - delta); scale applied at the end ----
             const bool need_mask = MASK && ((k0 + BN > p.Sk) || (CAUSAL && k0 + BN - 1 > qw0));
+            // stored keep bits: key k0 + 8 g + 4 hi + e at bit 8 g + e after the shift
+            const uint32_t km = DROPOUT == 2 ? kword >> (4 * hi) : 0u;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = k0 + 8 * (r >> 2) + 4 * hi + (r & 3);
@@ -607,7 +634,9 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
                 if (need_mask && (key >= p.Sk || (CAUSAL && key > qi))) pv = 0.f;
                 float dpv = dp[r];
                 if (DROPOUT) {
-                    dpv *= philox_keep(p.seed, row_ctr + (uint64_t)key, p.keep_thresh) ? p.rp : 0.f;
+                    const bool keep = DROPOUT == 2 ? ((km >> (8 * (r >> 2) + (r & 3))) & 1u) != 0u
+                                                   : philox_keep(p.seed, row_ctr + (uint64_t)key, p.keep_thresh);
+                    dpv *= keep ? p.rp : 0.f;
                 }
                 s[r] = pv * (dpv - del);
             }
@@ -690,7 +719,7 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
 }
 
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool CAUSAL, bool DROPOUT, typename TB>
+template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
 hipError_t launch_bwd_t(const BwdParams& p, int stage, hipStream_t s) {
     if (stage < 0 || stage == 0) {
         constexpr int EPC = 16 / sizeof(T);
@@ -716,17 +745,24 @@ hipError_t launch_bwd_t(const BwdParams& p, int stage, hipStream_t s) {
 
 template <typename T, typename TB>
 hipError_t launch_bwd_dispatch(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s) {
-#define FA_BWD_CASE(DD)                                                                  \
-    if (D == DD) {                                                                       \
-        if (causal) return dropout ? launch_bwd_t<T, DD, true, true, TB>(p, stage, s)  \
-                                   : launch_bwd_t<T, DD, true, false, TB>(p, stage, s); \
-        return dropout ? launch_bwd_t<T, DD, false, true, TB>(p, stage, s)             \
-                       : launch_bwd_t<T, DD, false, false, TB>(p, stage, s);           \
+    // dropout mode: 0 none, 1 Philox mask regenerated, 2 the forward's keep bits read
+    const int mode = !dropout ? 0 : (p.kb != nullptr ? 2 : 1);
+#define FA_BWD_MODES(DD, CC)                                                \
+    switch (mode) {                                                         \
+        case 0: return launch_bwd_t<T, DD, CC, 0, TB>(p, stage, s);         \
+        case 1: return launch_bwd_t<T, DD, CC, 1, TB>(p, stage, s);         \
+        default: return launch_bwd_t<T, DD, CC, 2, TB>(p, stage, s);        \
+    }
+#define FA_BWD_CASE(DD)                                                     \
+    if (D == DD) {                                                          \
+        if (causal) FA_BWD_MODES(DD, true)                                  \
+        FA_BWD_MODES(DD, false)                                             \
     }
     FA_BWD_CASE(32)
     FA_BWD_CASE(64)
     FA_BWD_CASE(128)
 #undef FA_BWD_CASE
+#undef FA_BWD_MODES
     return hipErrorInvalidValue;
 }
 

@@ -98,6 +98,50 @@ __device__ FA_INLINE inline float pair_sum(float x) {
     pair_swap(x, a, b);
     return a + b;
 }
+__device__ FA_INLINE inline uint32_t pair_or(uint32_t x) {
+    float a, b;
+    pair_swap(__builtin_bit_cast(float, x), a, b);
+    return __builtin_bit_cast(uint32_t, a) | __builtin_bit_cast(uint32_t, b);
+}
+
+// x of lane `lane ^ S` (S = 1, 2, 4, 8, 16): DPP moves within rows of 16
+// lanes (quad permutes for 1 and 2; row shifts up / down, one per side, for
+// 4 and 8), v_permlane16_swap between the rows of each 32-lane half for 16
+template <int S>
+__device__ FA_INLINE inline uint32_t xor_lane(uint32_t x, int lane) {
+    const int v = (int)x;
+    if constexpr (S == 1) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (S == 2) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (S == 4 || S == 8) {
+        const int up = __builtin_amdgcn_update_dpp(v, v, 0x100 + S, 0xF, 0xF, false);  // row_shl: lane + S
+        const int dn = __builtin_amdgcn_update_dpp(v, v, 0x110 + S, 0xF, 0xF, false);  // row_shr: lane - S
+        return (uint32_t)((lane & S) ? dn : up);
+    } else {
+        static_assert(S == 16, "lane distance");
+        const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        // r[0] holds lane - 16 in the odd rows, r[1] lane + 16 in the even rows
+        return (lane & 16) ? (uint32_t)r[0] : (uint32_t)r[1];
+    }
+}
+
+// 32 x 32 bit-matrix transpose within each 32-lane half: lane L holds row
+// word w (bit j = element (L, j)); afterwards lane j holds column word j (bit
+// L = element (L, j)).  Stage S swaps the off-diagonal S x S blocks between
+// lanes L and L ^ S.
+template <int S, uint32_t M>
+__device__ FA_INLINE inline uint32_t transpose_stage(uint32_t w, int lane) {
+    const uint32_t o = xor_lane<S>(w, lane);
+    return (lane & S) ? ((w & ~M) | ((o >> S) & M)) : ((w & M) | ((o & M) << S));
+}
+__device__ FA_INLINE inline uint32_t transpose32(uint32_t w, int lane) {
+    w = transpose_stage<16, 0x0000FFFFu>(w, lane);
+    w = transpose_stage<8, 0x00FF00FFu>(w, lane);
+    w = transpose_stage<4, 0x0F0F0F0Fu>(w, lane);
+    w = transpose_stage<2, 0x33333333u>(w, lane);
+    return transpose_stage<1, 0x55555555u>(w, lane);
+}
 
 __device__ FA_INLINE inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -53,7 +53,7 @@ struct FwdCfg {
 };
 
 // TB: element type of the additive bias (T or float), void = no bias
-template <typename T, int D, bool CAUSAL, bool DROPOUT, typename TB>
+template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
 __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     using C = FwdCfg<T, D>;
     constexpr bool BIAS = !std::is_void<TB>::value;
@@ -232,13 +232,23 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
             }
         l_run += psum;
         if (DROPOUT) {
+            constexpr bool bits_out = DROPOUT == 2;
 #pragma unroll
-            for (int blk = 0; blk < NB; ++blk)
+            for (int blk = 0; blk < NB; ++blk) {
+                uint32_t mine = 0;  // this lane's keep bits of the 32-key block
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int key = k0 + 32 * blk + 8 * (r >> 2) + 4 * hi + (r & 3);
-                    if (!philox_keep(p.seed, row_ctr + (uint64_t)key, p.keep_thresh)) s[blk][r] = 0.f;
+                    const int kk = 8 * (r >> 2) + 4 * hi + (r & 3);
+                    const bool keep = philox_keep(p.seed, row_ctr + (uint64_t)(k0 + 32 * blk + kk), p.keep_thresh);
+                    if (!keep) s[blk][r] = 0.f;
+                    if (bits_out) mine |= (uint32_t)keep << kk;
                 }
+                if (bits_out) {
+                    const uint32_t word = pair_or(mine);
+                    const int kw = (k0 >> 5) + blk;
+                    if (hi == 0 && qi < p.Sq && k0 + 32 * blk < p.Sk) p.kb[((int64_t)(b * p.H + h) * p.Sq + qi) * p.kb_w + kw] = word;
+                }
+            }
         }
         if constexpr (!C::F32) {
 #pragma unroll
@@ -400,7 +410,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     }
 }
 
-template <typename T, int D, bool CAUSAL, bool DROPOUT, typename TB>
+template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
 hipError_t launch_fwd_t(const FwdParams& p, hipStream_t s) {
     using C = FwdCfg<T, D>;
     FwdParams q = p;
@@ -413,17 +423,24 @@ hipError_t launch_fwd_t(const FwdParams& p, hipStream_t s) {
 
 template <typename T, typename TB>
 hipError_t launch_fwd_dispatch(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s) {
-#define FA_FWD_CASE(DD)                                                                  \
-    if (D == DD) {                                                                       \
-        if (causal) return dropout ? launch_fwd_t<T, DD, true, true, TB>(p, s)         \
-                                   : launch_fwd_t<T, DD, true, false, TB>(p, s);       \
-        return dropout ? launch_fwd_t<T, DD, false, true, TB>(p, s)                    \
-                       : launch_fwd_t<T, DD, false, false, TB>(p, s);                  \
+    // dropout mode: 0 none, 1 Philox mask, 2 Philox mask also written as keep bits
+    const int mode = !dropout ? 0 : (p.kb != nullptr ? 2 : 1);
+#define FA_FWD_MODES(DD, CC)                                                \
+    switch (mode) {                                                         \
+        case 0: return launch_fwd_t<T, DD, CC, 0, TB>(p, s);                \
+        case 1: return launch_fwd_t<T, DD, CC, 1, TB>(p, s);                \
+        default: return launch_fwd_t<T, DD, CC, 2, TB>(p, s);               \
+    }
+#define FA_FWD_CASE(DD)                                                     \
+    if (D == DD) {                                                          \
+        if (causal) FA_FWD_MODES(DD, true)                                  \
+        FA_FWD_MODES(DD, false)                                             \
     }
     FA_FWD_CASE(32)
     FA_FWD_CASE(64)
     FA_FWD_CASE(128)
 #undef FA_FWD_CASE
+#undef FA_FWD_MODES
     return hipErrorInvalidValue;
 }
 

@@ -27,6 +27,10 @@ struct FwdParams {
     float rp;          // 1 / (1 - dropout_p)
     uint32_t keep_thresh;  // keep_threshold(dropout_p)
     uint64_t seed, offset;
+    // optional dropout keep bits written for the backward: kb_w = ceil(Sk/32)
+    // words per query row, bit j%32 of word j/32 for key j
+    uint32_t* kb;
+    int kb_w;
     // optional additive bias (B, H, Sq, Sk) in the input dtype or float32; a
     // zero stride broadcasts that dimension, the key stride is 1
     const void* bias;
@@ -62,6 +66,8 @@ struct BwdParams {
     float scale, scale_log2, dropout_p, rp;
     uint32_t keep_thresh;  // keep_threshold(dropout_p)
     uint64_t seed, offset;
+    const uint32_t* kb;  // optional keep bits from the forward (as in FwdParams)
+    int kb_w;
     const void* bias;  // as in FwdParams
     int64_t bias_sb, bias_sh, bias_ss;
     int bias_span;

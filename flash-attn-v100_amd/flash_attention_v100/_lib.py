@@ -49,6 +49,7 @@ class FwdArgs(ctypes.Structure):
         ("scale", ctypes.c_float), ("dropout_p", ctypes.c_float),
         ("seed", ctypes.c_uint64), ("offset", ctypes.c_uint64),
         ("bias", ctypes.c_void_p), ("bias_stride", _I64x4), ("bias_dtype", ctypes.c_int32),
+        ("keep_bits", ctypes.c_void_p),
     ]
 
 
@@ -66,6 +67,7 @@ class BwdArgs(ctypes.Structure):
         ("seed", ctypes.c_uint64), ("offset", ctypes.c_uint64),
         ("bias", ctypes.c_void_p), ("bias_stride", _I64x4), ("bias_dtype", ctypes.c_int32),
         ("dbias", ctypes.c_void_p), ("dbias_stride", _I64x4), ("dbias_dtype", ctypes.c_int32),
+        ("keep_bits", ctypes.c_void_p),
     ]
 
 
@@ -211,7 +213,29 @@ def reduce_dbias(dbias: torch.Tensor, pb: PreparedBias) -> torch.Tensor:
     return g.to(pb.dtype)
 
 
-def fwd_args(q, k, v, o, lse, max_vals, causal, scale, dropout_p, seed, offset, bias=None) -> FwdArgs:
+# The dropout keep mask a forward applied, bit-packed: int32 words (B*H*Sq,
+# ceil(Sk/32)), bit j%32 of word j/32 of row (b*H + h)*Sq + i.  The autograd
+# function keeps it for the backward (one Philox pass instead of three) when it
+# takes at most this many bytes.
+KEEP_BITS_MAX_BYTES = 4 << 30
+
+
+def keep_bits_bytes(B: int, H: int, Sq: int, Sk: int) -> int:
+    return 4 * B * H * Sq * ((Sk + 31) // 32)
+
+
+def alloc_keep_bits(B: int, H: int, Sq: int, Sk: int, device) -> torch.Tensor:
+    return torch.empty((B * H * Sq, (Sk + 31) // 32), device=device, dtype=torch.int32)
+
+
+def _check_keep_bits(bits: torch.Tensor, B, H, Sq, Sk, device):
+    want = (B * H * Sq, (Sk + 31) // 32)
+    if bits.dtype != torch.int32 or tuple(bits.shape) != want or not bits.is_contiguous() or bits.device != device:
+        raise ValueError(f"keep bits must be a contiguous int32 {want} tensor on {device}")
+
+
+def fwd_args(q, k, v, o, lse, max_vals, causal, scale, dropout_p, seed, offset, bias=None,
+             keep_bits=None) -> FwdArgs:
     B, Sq, H, D = q.shape
     return FwdArgs(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
@@ -221,7 +245,8 @@ def fwd_args(q, k, v, o, lse, max_vals, causal, scale, dropout_p, seed, offset, 
         float(scale), float(dropout_p), seed, offset,
         bias.tensor.data_ptr() if bias is not None else None,
         bias.strides if bias is not None else _I64x4(0, 0, 0, 1),
-        bias.dtype_code if bias is not None else DTYPE_CODES[q.dtype])
+        bias.dtype_code if bias is not None else DTYPE_CODES[q.dtype],
+        keep_bits.data_ptr() if keep_bits is not None else None)
 
 
 def _as_prepared(bias, q, k) -> Optional[PreparedBias]:
@@ -231,9 +256,12 @@ def _as_prepared(bias, q, k) -> Optional[PreparedBias]:
 
 
 def fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: float,
-        dropout_p: float = 0.0, seed: int = 0, offset: int = 0, want_max: bool = False, bias=None):
+        dropout_p: float = 0.0, seed: int = 0, offset: int = 0, want_max: bool = False, bias=None,
+        keep_bits: Optional[torch.Tensor] = None):
     """Run ``fa_fwd``: returns (o, lse, max_vals or None).  Inputs (B, S, H, D);
-    ``bias`` a (B|1, H|1, Sq|1, Sk) tensor or a :class:`PreparedBias`."""
+    ``bias`` a (B|1, H|1, Sq|1, Sk) tensor or a :class:`PreparedBias`;
+    ``keep_bits`` (from :func:`alloc_keep_bits`, with dropout) receives the
+    keep mask applied."""
     lib = load()
     q, k, v = prepare(q), prepare(k), prepare(v)
     pb = _as_prepared(bias, q, k)
@@ -241,13 +269,15 @@ def fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: 
     o = torch.empty_like(q, memory_format=torch.contiguous_format)
     lse = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32)
     mx = torch.empty((B, H, Sq), device=q.device, dtype=torch.float32) if want_max else None
-    a = fwd_args(q, k, v, o, lse, mx, causal, scale, dropout_p, seed, offset, pb)
+    if keep_bits is not None:
+        _check_keep_bits(keep_bits, B, H, Sq, k.shape[1], q.device)
+    a = fwd_args(q, k, v, o, lse, mx, causal, scale, dropout_p, seed, offset, pb, keep_bits)
     _check("fa_fwd", lib.fa_fwd(ctypes.byref(a), _stream(q)))
     return o, lse, mx
 
 
 def bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, offset,
-             bias=None, dbias=None) -> BwdArgs:
+             bias=None, dbias=None, keep_bits=None) -> BwdArgs:
     B, Sq, H, D = q.shape
     return BwdArgs(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr(), lse.data_ptr(),
@@ -261,7 +291,8 @@ def bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, of
         bias.dtype_code if bias is not None else DTYPE_CODES[q.dtype],
         dbias.data_ptr() if dbias is not None else None,
         _dbias_strides(dbias) if dbias is not None else _I64x4(0, 0, 0, 1),
-        DTYPE_CODES[dbias.dtype] if dbias is not None else DTYPE_CODES[torch.float32])
+        DTYPE_CODES[dbias.dtype] if dbias is not None else DTYPE_CODES[torch.float32],
+        keep_bits.data_ptr() if keep_bits is not None else None)
 
 
 def _dbias_strides(dbias):
@@ -271,9 +302,12 @@ def _dbias_strides(dbias):
 
 
 def bwd(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float = 0.0,
-        seed: int = 0, offset: int = 0, bias=None, want_dbias: bool = False):
+        seed: int = 0, offset: int = 0, bias=None, want_dbias: bool = False,
+        keep_bits: Optional[torch.Tensor] = None):
     """Run ``fa_bwd``: returns (dq, dk, dv) in the input dtype, plus the bias
-    gradient in the caller's bias shape and dtype when ``want_dbias``."""
+    gradient in the caller's bias shape and dtype when ``want_dbias``.
+    ``keep_bits``: the mask the forward wrote (same seed / offset), read
+    instead of regenerating it."""
     lib = load()
     q, k, v, o, do = (prepare(t) for t in (q, k, v, o, do))
     pb = _as_prepared(bias, q, k)
@@ -298,7 +332,9 @@ def bwd(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float = 0.0,
             dbias = torch.empty((B, H, Sq, Sk), device=q.device, dtype=gdt)
         else:
             dbias = torch.empty((Bo, Ho, Sq, -(-Sk // 4) * 4), device=q.device, dtype=gdt)[..., :Sk]
-    a = bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, offset, pb, dbias)
+    if keep_bits is not None:
+        _check_keep_bits(keep_bits, q.shape[0], q.shape[2], q.shape[1], k.shape[1], q.device)
+    a = bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, offset, pb, dbias, keep_bits)
     ws_bytes = lib.fa_bwd_workspace_size(ctypes.byref(a))
     ws = torch.empty(max(int(ws_bytes), 256), device=q.device, dtype=torch.uint8)
     _check("fa_bwd", lib.fa_bwd(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(q)))

@@ -104,7 +104,13 @@ class EnhancedFlashAttentionV100Function(torch.autograd.Function):
             scale = q.shape[-1] ** -0.5
         pb = _prepare_bias(bias, q, k)
         seed, offset = _lib.seed_offset(dropout_seed, dropout_offset) if dropout_p > 0 else (0, 0)
-        o, lse, _ = _lib.fwd(q, k, v, causal, scale, dropout_p, seed, offset, bias=pb)
+        bits = None
+        if dropout_p > 0 and any(ctx.needs_input_grad[:3] + ctx.needs_input_grad[6:7]):
+            B, Sq, H, _ = q.shape
+            if _lib.keep_bits_bytes(B, H, Sq, k.shape[1]) <= _lib.KEEP_BITS_MAX_BYTES:
+                bits = _lib.alloc_keep_bits(B, H, Sq, k.shape[1], q.device)
+        o, lse, _ = _lib.fwd(q, k, v, causal, scale, dropout_p, seed, offset, bias=pb, keep_bits=bits)
+        ctx.keep_bits = bits
         if pb is None:
             ctx.save_for_backward(q, k, v, o, lse)
         else:
@@ -131,7 +137,9 @@ class EnhancedFlashAttentionV100Function(torch.autograd.Function):
         pb = None if ctx.bias_meta is None else _lib.PreparedBias(saved[5], *ctx.bias_meta)
         want_dbias = pb is not None and ctx.needs_input_grad[6]
         grads = _lib.bwd(q, k, v, o, grad_output, lse, ctx.causal, ctx.scale,
-                         ctx.dropout_p, ctx.seed, ctx.offset, bias=pb, want_dbias=want_dbias)
+                         ctx.dropout_p, ctx.seed, ctx.offset, bias=pb, want_dbias=want_dbias,
+                         keep_bits=ctx.keep_bits)
+        ctx.keep_bits = None
         dq, dk, dv = grads[:3]
         return (
             dq if ctx.needs_input_grad[0] else None,

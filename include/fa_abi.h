@@ -20,6 +20,13 @@
  * multiples of 16 bytes, and the base 16-byte aligned.  It is added in fp32 to
  * the scaled scores before the causal mask (reference
  * forward_kernel.py:166-182).
+ *
+ * Optional dropout keep bits (NULL = none; ignored when dropout_p == 0): the
+ * forward writes the keep mask it applied, and the backward given them reads
+ * it instead of regenerating the Philox stream (same mask, same results).
+ * keep_bits: 4-byte aligned uint32 words, row ((b*H + h)*Sq + i) of
+ * ceil(Sk/32) words, bit j%32 of word j/32 = keep(b, h, i, j); words whose 32
+ * keys causal masking removes for query i are left unwritten (and unread).
  */
 #ifndef FA_ABI_H
 #define FA_ABI_H
@@ -93,6 +100,7 @@ typedef struct fa_fwd_args {
     const void* bias;        /* optional additive bias (NULL = none), see the file comment */
     int64_t bias_stride[4];  /* (b, h, i, j) in elements */
     int32_t bias_dtype;      /* dtype, or FA_DTYPE_F32 */
+    uint32_t* keep_bits;     /* optional dropout keep bits out, see the file comment */
 } fa_fwd_args;
 
 /* Backward arguments.
@@ -146,6 +154,7 @@ typedef struct fa_bwd_args {
     void* dbias;              /* optional (B, H, Sq, Sk) gradient of the bias, fully written */
     int64_t dbias_stride[4];  /* (b, h, i, j) in elements; j stride 1, i stride >= Sk; b, h: 0 = sum */
     int32_t dbias_dtype;      /* FA_DTYPE_* of dbias */
+    const uint32_t* keep_bits;  /* optional: the forward's dropout keep bits (file comment) */
 } fa_bwd_args;
 
 /* Library ABI version (FA_ABI_VERSION).  No reference counterpart. */

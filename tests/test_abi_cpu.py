@@ -59,11 +59,12 @@ int main(void) {
   F(fa_fwd_args, q) F(fa_fwd_args, max_vals) F(fa_fwd_args, q_stride) F(fa_fwd_args, o_stride)
   F(fa_fwd_args, batch) F(fa_fwd_args, causal) F(fa_fwd_args, scale) F(fa_fwd_args, dropout_p)
   F(fa_fwd_args, seed) F(fa_fwd_args, offset) F(fa_fwd_args, bias) F(fa_fwd_args, bias_stride)
-  F(fa_fwd_args, bias_dtype)
+  F(fa_fwd_args, bias_dtype) F(fa_fwd_args, keep_bits)
   F(fa_bwd_args, dout) F(fa_bwd_args, lse) F(fa_bwd_args, dv) F(fa_bwd_args, do_stride)
   F(fa_bwd_args, dv_stride) F(fa_bwd_args, batch) F(fa_bwd_args, causal) F(fa_bwd_args, scale)
   F(fa_bwd_args, seed) F(fa_bwd_args, offset) F(fa_bwd_args, bias) F(fa_bwd_args, bias_stride)
   F(fa_bwd_args, bias_dtype) F(fa_bwd_args, dbias) F(fa_bwd_args, dbias_stride) F(fa_bwd_args, dbias_dtype)
+  F(fa_bwd_args, keep_bits)
   return 0;
 }
 """
@@ -253,6 +254,29 @@ def test_bwd_check_dbias_rules():
     assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_OK"]
     a.dbias = a.dbias + 1  # not element-aligned
     assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_ERR_BIAS"]
+
+
+def test_keep_bits_rules():
+    lib = _lib.load()
+    B, S, H, D = 2, 100, 3, 64
+    bits = _lib.alloc_keep_bits(B, H, S, S, "cpu")
+    assert bits.shape == (B * H * S, 4) and bits.dtype == torch.int32
+    assert _lib.keep_bits_bytes(B, H, S, S) == 4 * bits.numel()
+    a, _keep = _cpu_fwd(B=B, Sq=S, Sk=S, H=H, Hkv=H, D=D)
+    a.dropout_p = 0.1
+    a.keep_bits = bits.data_ptr()
+    assert _status(a) == CODES["FA_OK"]
+    a.keep_bits = bits.data_ptr() + 2
+    assert _status(a) == CODES["FA_ERR_ALIGN"]
+    q = torch.zeros(B, S, H, D, dtype=torch.bfloat16)
+    lse = torch.zeros(B, H, S)
+    a = _lib.bwd_args(q, q, q, q, q, lse, q, q, q, True, 0.125, 0.1, 0, 0, keep_bits=bits)
+    ws = lib.fa_bwd_workspace_size(ctypes.byref(a))
+    assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_OK"]
+    a.keep_bits = bits.data_ptr() + 6
+    assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_ERR_ALIGN"]
+    with pytest.raises(ValueError):
+        _lib._check_keep_bits(_lib.alloc_keep_bits(B, H, S, S + 40, "cpu"), B, H, S, S, torch.device("cpu"))
 
 
 def test_prepare_bias_layout():
