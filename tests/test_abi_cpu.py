@@ -88,6 +88,18 @@ def test_ctypes_structs_match_header():
         assert getattr(cls, m).offset == off, (s, m)
 
 
+def test_integration_stub_struct_matches_header():
+    # the ctypes stub a maintainer would copy into the reference must carry every
+    # field: a shorter struct makes the library read past its end
+    text = open(os.path.join(REPO, "INTEGRATION.md")).read()
+    m = re.search(r"class fa_fwd_args\(ctypes.Structure\):.*?_fields_ = (\[.*?\])\s*(?:#[^\n]*)?\n", text, flags=re.S)
+    assert m, "stub struct not found"
+    fields = eval(m.group(1), {"ctypes": ctypes, "_I64x4": ctypes.c_int64 * 4})
+    stub = type("Stub", (ctypes.Structure,), {"_fields_": fields})
+    assert ctypes.sizeof(stub) == ctypes.sizeof(_lib.FwdArgs)
+    assert [f[0] for f in fields] == [f[0] for f in _lib.FwdArgs._fields_]
+
+
 def test_strerror_names_every_code():
     for name, code in CODES.items():
         msg = _lib.strerror(code)
