@@ -146,7 +146,9 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
     const float c = p.scale_log2;
 
     // query tiles: causal needs queries >= k0 only; per query head of the
-    // group, the first tiles cross this wave's keys and are masked
+    // group the tiles run from the last one down, so that all workgroups of a
+    // head read the same Q / dO tiles at about the same time (L2 reuse), and
+    // the final tiles of the run cross this wave's keys and are masked
     const int qt_begin = CAUSAL ? (k0 / BQ) : 0;
     const int qt_end = (p.Sq + BQ - 1) / BQ;
     const int nq = qt_end > qt_begin ? qt_end - qt_begin : 0;
@@ -163,7 +165,7 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
     static_assert(BQ == 64, "one dword per lane for each of LSE and delta");
     auto buf = [&](int s) -> char* { return smem + s * C::BUF_BYTES; };
     auto tile_head = [&](int it) { return hk * p.group + it / nq; };
-    auto tile_q0 = [&](int it) { return (qt_begin + it % nq) * BQ; };
+    auto tile_q0 = [&](int it) { return (qt_end - 1 - it % nq) * BQ; };
     auto issue = [&](int it, int s) FA_INLINE {
         const int hh = tile_head(it), qb0 = tile_q0(it);
         char* bp = buf(s);
@@ -412,12 +414,12 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
         }
     }
 
-    // masked tiles first for each query head of the group, then plain ones
+    // plain tiles first for each query head of the group, then the masked ones
     int it = 0;
     for (int g = 0; g < p.group; ++g) {
+        for (; it < g * nq + (nq - n_mask); ++it) iter(it, std::false_type{});
         if (CAUSAL)
-            for (; it < g * nq + n_mask; ++it) iter(it, std::true_type{});
-        for (; it < (g + 1) * nq; ++it) iter(it, std::false_type{});
+            for (; it < (g + 1) * nq; ++it) iter(it, std::true_type{});
     }
 
     // ---- epilogue: stage dK^T, dV^T through LDS as rows, coalesced stores ----
