@@ -369,8 +369,9 @@ struct DmaTile {
 #pragma unroll
         for (int t = 0; t < PER; ++t) {
             const int c = 64 * (wave + NW * t) + lane;
-            const int row = c / CW, col = min(c % CW, CD - 1);
-            off[t] = (row * (int)row_stride + col * EPC) * (int)sizeof(T);
+            const int row = c / CW, col = c % CW;
+            // padding chunks of an LDS row read nothing (out of the buffer's range)
+            off[t] = col < CD ? (row * (int)row_stride + col * EPC) * (int)sizeof(T) : kOffNowhere;
         }
     }
     __device__ FA_INLINE inline void load(const T* base, int64_t row_stride, int nvalid, T* lds, int lane) const {
@@ -409,8 +410,8 @@ struct DmaRows {
 #pragma unroll
         for (int t = 0; t < PER; ++t) {
             const int c = 64 * (wave + NWAVES * t) + lane;
-            const int row = c / CW, col = min(c % CW, CD - 1);
-            off[t] = (row * (int)row_stride + col * EPC) * (int)sizeof(T);
+            const int row = c / CW, col = c % CW;
+            off[t] = col < CD ? (row * (int)row_stride + col * EPC) * (int)sizeof(T) : kOffNowhere;
         }
     }
     // copies this wave's instructions [T0, T1) of the tile
@@ -444,8 +445,10 @@ struct DmaRowGroups {
     __device__ FA_INLINE inline void init(int64_t row_stride, int lane, int wave_id) {
         wave = wave_id;
         rowl = lane < KR * CW ? lane / CW : KR;
-        const int col = min(lane % CW, CD - 1);
-        off = ((lane / CW) * (int)row_stride + col * EPC) * (int)sizeof(T);
+        // padding chunks read nothing: an offset past the range stays past it
+        // after the group's row step is added (slices span < 2^31 bytes)
+        const int col = lane % CW;
+        off = col < CD ? ((lane / CW) * (int)row_stride + col * EPC) * (int)sizeof(T) : kOffNowhere;
     }
     __device__ FA_INLINE inline void load(const T* base, int64_t row_stride, int nvalid, T* lds) const {
         const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D>(base, row_stride, nvalid);
