@@ -6,8 +6,9 @@ the same 19 leading positional inputs, the same saved-tensor contract
 (``save_for_backward`` of the inputs, output and LSE, ``:212``), ``(output, lse)``
 when ``return_softmax_lse`` and one gradient slot per input in ``backward``
 (``:313-333``).  Two optional trailing inputs carry the dropout Philox seed and
-offset so the backward regenerates the forward's mask (the reference never saved
-them, ``:209-227``).
+offset so the backward can reproduce the forward's mask (the reference never
+saved them, ``:209-227``); with dropout the forward also keeps the mask as bits
+for the backward when they fit ``_lib.KEEP_BITS_MAX_BYTES``.
 
 An additive ``bias`` of shape (B|1, H|1, Sq|1, Sk) is added to the scaled
 scores inside the kernels (reference ``kernels/forward_kernel.py:166-182``)
@@ -15,11 +16,19 @@ and, when the bias requires grad, its real gradient dS (summed over broadcast
 dimensions) is returned in the bias slot; the reference returned zeros there
 (``ops/attention.py:297-301``).
 
+``enable_gradient_checkpointing`` (or a :func:`gradient_checkpointing_mode`
+region) keeps only q, k, v and the LSE: the backward recomputes the output with
+one forward pass (deterministic, so the gradients are bit-identical) instead of
+holding it between the passes, which saves B*Sq*H*D elements per call.  The
+reference recomputed the forward per query segment for dq and ran the full
+backward for dk, dv (``ops/attention.py:409-461``), with the same results;
+``num_checkpoints`` has no role here and is ignored, and the reference's
+automatic switch-on at a 14 GB memory estimate (``:110-124``) is not copied.
+
 Deliberate differences, each raising instead of silently computing something
 else: multi-GPU execution is out of scope (``NotImplementedError``);
-``enable_gradient_checkpointing`` is accepted and has nothing to do (the
-backward already recomputes P tile by tile); ``block_size_m/n`` are validated
-hints, the gfx950 tile shape is fixed per (dtype, head_dim).
+``block_size_m/n`` are validated hints, the gfx950 tile shape is fixed per
+(dtype, head_dim).
 """
 from __future__ import annotations
 
@@ -68,6 +77,19 @@ def _prepare_bias(bias, q, k):
     return _lib.prepare_bias(bias, q.shape[0], q.shape[2], q.shape[1], k.shape[1], q.dtype)
 
 
+# set by gradient_checkpointing_mode()
+_CHECKPOINTING = False
+
+
+def _keep_bits_for(q, k):
+    """A keep-bit buffer for the dropout mask of these inputs, or None past
+    ``_lib.KEEP_BITS_MAX_BYTES`` (the backward then regenerates the mask)."""
+    B, Sq, H, _ = q.shape
+    if _lib.keep_bits_bytes(B, H, Sq, k.shape[1]) > _lib.KEEP_BITS_MAX_BYTES:
+        return None
+    return _lib.alloc_keep_bits(B, H, Sq, k.shape[1], q.device)
+
+
 class EnhancedFlashAttentionV100Function(torch.autograd.Function):
     """FlashAttention forward/backward on the gfx950 HIP kernels."""
 
@@ -104,17 +126,15 @@ class EnhancedFlashAttentionV100Function(torch.autograd.Function):
             scale = q.shape[-1] ** -0.5
         pb = _prepare_bias(bias, q, k)
         seed, offset = _lib.seed_offset(dropout_seed, dropout_offset) if dropout_p > 0 else (0, 0)
+        recompute = bool(enable_gradient_checkpointing) or _CHECKPOINTING
         bits = None
-        if dropout_p > 0 and any(ctx.needs_input_grad[:3] + ctx.needs_input_grad[6:7]):
-            B, Sq, H, _ = q.shape
-            if _lib.keep_bits_bytes(B, H, Sq, k.shape[1]) <= _lib.KEEP_BITS_MAX_BYTES:
-                bits = _lib.alloc_keep_bits(B, H, Sq, k.shape[1], q.device)
+        if dropout_p > 0 and not recompute and any(ctx.needs_input_grad[:3] + ctx.needs_input_grad[6:7]):
+            bits = _keep_bits_for(q, k)
         o, lse, _ = _lib.fwd(q, k, v, causal, scale, dropout_p, seed, offset, bias=pb, keep_bits=bits)
         ctx.keep_bits = bits
-        if pb is None:
-            ctx.save_for_backward(q, k, v, o, lse)
-        else:
-            ctx.save_for_backward(q, k, v, o, lse, pb.tensor)
+        ctx.recompute_output = recompute
+        kept = (q, k, v, lse) if recompute else (q, k, v, o, lse)
+        ctx.save_for_backward(*kept, *(() if pb is None else (pb.tensor,)))
         ctx.bias_meta = None if pb is None else (pb.strides, pb.dtype_code, pb.shape, pb.dtype)
         ctx.scale = scale
         ctx.causal = causal
@@ -133,12 +153,23 @@ class EnhancedFlashAttentionV100Function(torch.autograd.Function):
     def backward(ctx, grad_output: torch.Tensor, grad_softmax_lse: Optional[torch.Tensor] = None):
         # grad_softmax_lse is ignored, as in the reference (ops/attention.py:234-333)
         saved = ctx.saved_tensors
-        q, k, v, o, lse = saved[:5]
-        pb = None if ctx.bias_meta is None else _lib.PreparedBias(saved[5], *ctx.bias_meta)
+        n = 4 if ctx.recompute_output else 5
+        pb = None if ctx.bias_meta is None else _lib.PreparedBias(saved[n], *ctx.bias_meta)
+        bits = ctx.keep_bits
+        if ctx.recompute_output:
+            # the output again, from the same inputs, seed and offset (same bits);
+            # the recomputing pass also records the dropout mask for the backward
+            q, k, v, lse = saved[:4]
+            if ctx.dropout_p > 0:
+                bits = _keep_bits_for(q, k)
+            o = _lib.fwd(q, k, v, ctx.causal, ctx.scale, ctx.dropout_p, ctx.seed, ctx.offset,
+                         bias=pb, keep_bits=bits)[0]
+        else:
+            q, k, v, o, lse = saved[:5]
         want_dbias = pb is not None and ctx.needs_input_grad[6]
         grads = _lib.bwd(q, k, v, o, grad_output, lse, ctx.causal, ctx.scale,
                          ctx.dropout_p, ctx.seed, ctx.offset, bias=pb, want_dbias=want_dbias,
-                         keep_bits=ctx.keep_bits)
+                         keep_bits=bits)
         ctx.keep_bits = None
         dq, dk, dv = grads[:3]
         return (
@@ -299,9 +330,17 @@ def compare_with_pytorch_attention_enhanced(
 
 @contextlib.contextmanager
 def gradient_checkpointing_mode(enable: bool = True):
-    """Accepted for compatibility (reference ``ops/attention.py:721-726``, a
-    placeholder there too): the backward already recomputes P tile by tile."""
-    yield
+    """Within the region, attention calls keep only q, k, v and the LSE and
+    recompute the output in the backward (as ``enable_gradient_checkpointing``
+    does per call).  The reference's context manager is a placeholder
+    (``ops/attention.py:721-726``)."""
+    global _CHECKPOINTING
+    prev = _CHECKPOINTING
+    _CHECKPOINTING = bool(enable)
+    try:
+        yield
+    finally:
+        _CHECKPOINTING = prev
 
 
 @contextlib.contextmanager

@@ -178,3 +178,39 @@ def test_standalone_forward_backward_and_compare():
             f"cos {r['cosine_similarity']:.6f}")
         assert r["allclose"] and r["cosine_similarity"] > 0.9999
         assert r["configuration"]["has_bias"] == (b is not None) and r["input_shape"] == q.shape
+
+
+@pytest.mark.parametrize("dtype,causal,p,with_bias,Hkv", [
+    (torch.bfloat16, True, 0.0, False, 4),
+    (torch.float16, True, 0.1, True, 2),     # dropout (bits made by the recomputing pass) + bias grad + GQA
+    (torch.float32, False, 0.2, False, 4),
+])
+def test_gradient_checkpointing_recomputes_output(dtype, causal, p, with_bias, Hkv):
+    # enable_gradient_checkpointing keeps q, k, v and the LSE only and recomputes
+    # the output in the backward: every gradient equals the stored-output path's
+    B, S, H, D = 2, 200, 4, 64
+    say(f"case: checkpointing {dtype} causal={causal} p={p} bias={with_bias} Hkv={Hkv}")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, S, H, D, dtype, Hkv=Hkv, seed=17))
+    bias = torch.randn(1, H, S, S, device=DEV).to(dtype) if with_bias else None
+    runs = []
+    for ckpt in (False, True):
+        qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+        bb = bias.clone().requires_grad_(True) if with_bias else None
+        o = fa.FlashAttentionV100Function.apply(qq, kk, vv, D ** -0.5, causal, p, bb, None, None, True, False,
+                                                ckpt, True, None, True, "balanced", False, 1, 0, 99, 7)
+        saved_ptrs = {t.data_ptr() for t in o.grad_fn.saved_tensors}
+        assert (o.data_ptr() in saved_ptrs) == (not ckpt)
+        o.backward(do)
+        torch.cuda.synchronize()
+        runs.append([o.detach(), qq.grad, kk.grad, vv.grad] + ([bb.grad] if with_bias else []))
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    # the context manager switches it on for calls inside the region
+    with fa.ops.attention.gradient_checkpointing_mode():
+        qq = q.clone().requires_grad_(True)
+        o = fa.flash_attention_v100(qq, k, v, causal=causal, dropout_p=p, bias=bias, dropout_seed=99,
+                                    dropout_offset=7)
+        assert o.data_ptr() not in {t.data_ptr() for t in o.grad_fn.saved_tensors}
+        o.backward(do)
+    torch.cuda.synchronize()
+    assert torch.equal(qq.grad, runs[0][1])

@@ -66,8 +66,14 @@ def test_standalone_function_signatures_and_aliases():
     assert ops.flash_attention_forward is ops.flash_attention_forward_enhanced is fa.flash_attention_forward
     assert ops.flash_attention_backward is ops.flash_attention_backward_enhanced is fa.flash_attention_backward
     assert ops.compare_with_pytorch_attention is ops.compare_with_pytorch_attention_enhanced
+    from flash_attention_v100.ops import attention as att
+    assert not att._CHECKPOINTING
     with ops.gradient_checkpointing_mode(), ops.mixed_precision_mode(False):
-        pass
+        assert att._CHECKPOINTING
+        with ops.gradient_checkpointing_mode(False):
+            assert not att._CHECKPOINTING
+        assert att._CHECKPOINTING
+    assert not att._CHECKPOINTING
 
 
 def test_standalone_functions_reject_cpu_tensors():
