@@ -19,8 +19,13 @@ from the dK/dV kernel, accumulated in fp32; for ``heads`` its sum over the batch
 done by the library), inside the timed step.
 The FLOP count is the same (the bias adds no matrix products).
 
+With ``--all-configs`` it instead prints one JSON line per BASELINE config
+(C1-C5: GPU time and TFLOP/s of the config's pass, and the same CPU baseline on
+a bounded sample of that config); the dropout configs run the autograd
+default, the forward storing the keep bits that the backward reads.
+
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                    [--bias {none,full,heads}] [--dbias]
+                    [--bias {none,full,heads}] [--dbias] [--all-configs]
 """
 from __future__ import annotations
 
@@ -35,6 +40,7 @@ sys.path.insert(0, os.path.join(REPO, "flash-attn-v100_amd"))
 sys.path.insert(0, REPO)
 
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (AMD published)
+PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 MFMA
 PEAK_HBM_GBS = 8000.0
 METRIC = "attention TFLOP/s fwd & fwd+bwd, bf16 S=4096 D=128 causal; % of MFMA peak"
 B, S, H, D = 4, 4096, 32, 128
@@ -158,6 +164,113 @@ def cpu_baseline(target_s: float = 12.0, bias_kind: str = "none"):
             "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count()}
 
 
+# name, (B, S, H, D), dtype, causal, dropout p, with backward
+ALL_CONFIGS = [
+    ("C1", (2, 1024, 12, 64), "float16", False, 0.0, False),
+    ("C2", (2, 1024, 12, 64), "float16", True, 0.0, True),
+    ("C3", (4, 4096, 32, 128), "bfloat16", True, 0.0, True),
+    ("C4-causal", (1, 16384, 16, 128), "bfloat16", True, 0.0, True),
+    ("C4-full", (1, 16384, 16, 128), "bfloat16", False, 0.0, True),
+] + [(f"C5-D{d}-{'fp32' if dt == 'float32' else 'fp16'}", (8, 1000, 16, d), dt, True, 0.1, True)
+     for d in (32, 64, 128) for dt in ("float32", "float16")]
+
+
+def all_configs(n: int, cpu: bool, cpu_target_s: float = 3.0):
+    """One JSON line per BASELINE config: GPU time of its pass (HIP events,
+    mean of ``n`` calls) and, unless ``cpu`` is False, the fp32 math path of
+    oracle/ on this host for B=1 and as many heads as fit ``cpu_target_s``."""
+    import ctypes
+
+    import torch
+
+    from flash_attention_v100 import _lib
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+
+    def timed(fn):
+        fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / n  # ms
+
+    for name, (b, s, h, d), dts, causal, p, with_bwd in ALL_CONFIGS:
+        dt = getattr(torch, dts)
+        g = torch.Generator("cpu").manual_seed(42)
+        q, k, v, do = (torch.randn(b, s, h, d, generator=g).to(dt).cuda() for _ in range(4))
+        o = torch.empty_like(q)
+        lse = torch.empty(b, h, s, device="cuda")
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        bits = _lib.alloc_keep_bits(b, h, s, s, q.device) if p > 0 else None
+        fa = _lib.fwd_args(q, k, v, o, lse, None, causal, d ** -0.5, p, 42, 0, None, bits)
+        ba = _lib.bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, d ** -0.5, p, 42, 0, None, None, bits)
+        ws = torch.empty(max(256, lib.fa_bwd_workspace_size(ctypes.byref(ba))), device="cuda", dtype=torch.uint8)
+
+        def fwd():
+            st = lib.fa_fwd(ctypes.byref(fa), sp)
+            if st:
+                raise RuntimeError(_lib.strerror(st))
+
+        def bwd():
+            st = lib.fa_bwd(ctypes.byref(ba), ctypes.c_void_p(ws.data_ptr()), ws.numel(), sp)
+            if st:
+                raise RuntimeError(_lib.strerror(st))
+
+        fwd_ms = timed(fwd)
+        bwd_ms = timed(bwd) if with_bwd else None
+        F = f_fwd(b, h, s, d, causal)
+        flop = 3.5 * F if with_bwd else F
+        ms = fwd_ms + (bwd_ms or 0.0)
+        tf = flop / (ms * 1e-3) / 1e12
+        peak = PEAK_FP32_TFLOPS if dt == torch.float32 else PEAK_BF16_TFLOPS
+        out = {"config": name, "shape_bshd": [b, s, h, d], "dtype": dts, "causal": causal, "dropout_p": p,
+               "pass": "fwd+bwd" if with_bwd else "fwd", "fwd_ms": round(fwd_ms, 4),
+               "bwd_ms": None if bwd_ms is None else round(bwd_ms, 4), "tflops": round(tf, 2),
+               "pct_peak": round(100 * tf / peak, 2), "peak_tflops": peak,
+               "dropout_mask": "keep bits (forward writes, backward reads)" if p > 0 else None}
+        if cpu:
+            out["cpu_baseline"] = _cpu_sample(s, h, d, causal, p, with_bwd, cpu_target_s)
+        print(json.dumps(out), flush=True)
+        del q, k, v, do, o, lse, dq, dk, dv, bits, ws
+        torch.cuda.empty_cache()
+
+
+def _cpu_sample(s, h_max, d, causal, p, with_bwd, target_s):
+    """fp32 math path (oracle.attention) for B=1 and as many heads as fit
+    about ``target_s`` seconds; dropout applies a torch.rand mask (the CPU
+    path's cost, not the kernels' Philox stream)."""
+    import torch
+
+    from oracle import attention as oa
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator("cpu").manual_seed(42)
+
+    def run(h):
+        q, k, v, do = (torch.randn(1, s, h, d, generator=g) for _ in range(4))
+        keep = (torch.rand(1, h, s, s, generator=g) > p) if p > 0 else None
+        t0 = time.perf_counter()
+        if with_bwd:
+            oa.attention_autograd(q, k, v, do, causal, d ** -0.5, keep, p, dtype=torch.float32)
+        else:
+            oa.attention_forward(q, k, v, causal, d ** -0.5, keep, p, torch.float32)
+        return time.perf_counter() - t0
+
+    run(1)
+    t1 = run(1)
+    h = int(max(1, min(h_max, target_s / max(t1, 1e-3))))
+    t = min(run(h) for _ in range(2))
+    flop = f_fwd(1, h, s, d, causal) * (3.5 if with_bwd else 1.0)
+    return {"value": round(flop / t / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"B=1, H={h} in fp32 via oracle.attention; best of 2 runs, {t:.2f} s each"}
+
+
 def _cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -209,6 +322,8 @@ def main():
     ap.add_argument("--dbias", action="store_true", help="with --bias: also produce the bias gradient")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
+    ap.add_argument("--all-configs", action="store_true",
+                    help="one JSON line per BASELINE config (C1-C5) instead of the headline line")
     a = ap.parse_args()
     if a.copy_calibration:
         copy_calibration()
@@ -220,6 +335,9 @@ def main():
 
     if a.dbias and a.bias == "none":
         ap.error("--dbias needs --bias")
+    if a.all_configs:
+        all_configs(max(a.steps, 10), not a.no_cpu_baseline)
+        return
     r = gpu_bench(a.steps, a.warmup, a.bias, a.dbias)
     F = f_fwd()
     Ftot = 3.5 * F
