@@ -25,7 +25,7 @@ a bounded sample of that config); the dropout configs run the autograd
 default, the forward storing the keep bits that the backward reads.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                    [--bias {none,full,heads}] [--dbias] [--all-configs]
+                    [--bias {none,full,heads}] [--dbias] [--all-configs [--config NAME ...]]
 """
 from __future__ import annotations
 
@@ -175,7 +175,7 @@ ALL_CONFIGS = [
      for d in (32, 64, 128) for dt in ("float32", "float16")]
 
 
-def all_configs(n: int, cpu: bool, cpu_target_s: float = 3.0):
+def all_configs(n: int, cpu: bool, cpu_target_s: float = 3.0, only=None):
     """One JSON line per BASELINE config: GPU time of its pass (HIP events,
     mean of ``n`` calls) and, unless ``cpu`` is False, the fp32 math path of
     oracle/ on this host for B=1 and as many heads as fit ``cpu_target_s``."""
@@ -200,6 +200,8 @@ def all_configs(n: int, cpu: bool, cpu_target_s: float = 3.0):
         return e0.elapsed_time(e1) / n  # ms
 
     for name, (b, s, h, d), dts, causal, p, with_bwd in ALL_CONFIGS:
+        if only and name not in only:
+            continue
         dt = getattr(torch, dts)
         g = torch.Generator("cpu").manual_seed(42)
         q, k, v, do = (torch.randn(b, s, h, d, generator=g).to(dt).cuda() for _ in range(4))
@@ -324,6 +326,8 @@ def main():
                     help="only run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--all-configs", action="store_true",
                     help="one JSON line per BASELINE config (C1-C5) instead of the headline line")
+    ap.add_argument("--config", action="append", choices=[c[0] for c in ALL_CONFIGS],
+                    help="with --all-configs: only these configs (repeatable)")
     a = ap.parse_args()
     if a.copy_calibration:
         copy_calibration()
@@ -336,7 +340,7 @@ def main():
     if a.dbias and a.bias == "none":
         ap.error("--dbias needs --bias")
     if a.all_configs:
-        all_configs(max(a.steps, 10), not a.no_cpu_baseline)
+        all_configs(max(a.steps, 10), not a.no_cpu_baseline, only=a.config)
         return
     r = gpu_bench(a.steps, a.warmup, a.bias, a.dbias)
     F = f_fwd()
