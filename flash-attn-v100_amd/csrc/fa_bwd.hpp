@@ -289,18 +289,24 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
                 else
                     pv = fast_exp2(__builtin_fmaf(sc[r], c, -l4[e]));
                 if (MASK && q < kj) pv = 0.f;
+                // dropout: dropped entries of P and dP become 0; the 1 / (1 - p)
+                // of the kept ones goes into dS here and into dV's final scale
+                // (a 0 / 1 factor for the regenerated mask and a select for the
+                // stored one: the forms that spill least in each instantiation)
                 float dpv = dpc[r];
                 float pdv = pv;
-                if (DROPOUT) {
-                    const bool keep = DROPOUT == 2 ? ((km >> (8 * g + e)) & 1u) != 0u
-                                                   : philox_keep(p.seed, col_ctr + (uint64_t)q * (uint64_t)p.Sk,
-                                                                 p.keep_thresh);
-                    const float z = keep ? p.rp : 0.f;
+                if (DROPOUT == 1) {
+                    const float z =
+                        philox_keep(p.seed, col_ctr + (uint64_t)q * (uint64_t)p.Sk, p.keep_thresh) ? 1.f : 0.f;
                     dpv *= z;
                     pdv *= z;
+                } else if (DROPOUT == 2) {
+                    const bool keep = ((km >> (8 * g + e)) & 1u) != 0u;
+                    dpv = keep ? dpv : 0.f;
+                    pdv = keep ? pv : 0.f;
                 }
                 pd[r] = pdv;
-                ds[r] = pv * (dpv - d4[e]);
+                ds[r] = DROPOUT ? pv * __builtin_fmaf(dpv, p.rp, -d4[e]) : pv * (dpv - d4[e]);
             }
         }
         if (want_db) {
@@ -431,7 +437,7 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_k
     for (int pass = 0; pass < 2; ++pass) {
         sync_tiles();
         const f32x16* acc = pass == 0 ? dk : dv;
-        const float mul = pass == 0 ? p.scale : 1.f;
+        const float mul = pass == 0 ? p.scale : (DROPOUT ? p.rp : 1.f);
 #pragma unroll
         for (int i = 0; i < D / 32; ++i)
 #pragma unroll
@@ -634,13 +640,13 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
                 else
                     pv = fast_exp2(__builtin_fmaf(s[r], c, -lse2));
                 if (need_mask && (key >= p.Sk || (CAUSAL && key > qi))) pv = 0.f;
-                float dpv = dp[r];
                 if (DROPOUT) {
-                    const bool keep = DROPOUT == 2 ? ((km >> (8 * (r >> 2) + (r & 3))) & 1u) != 0u
-                                                   : philox_keep(p.seed, row_ctr + (uint64_t)key, p.keep_thresh);
-                    dpv *= keep ? p.rp : 0.f;
+                    const uint32_t m = DROPOUT == 2 ? bit_mask(km, 8 * (r >> 2) + (r & 3))
+                                       : (philox_keep(p.seed, row_ctr + (uint64_t)key, p.keep_thresh) ? ~0u : 0u);
+                    s[r] = pv * __builtin_fmaf(keep_or_zero(dp[r], m), p.rp, -del);
+                } else {
+                    s[r] = pv * (dp[r] - del);
                 }
-                s[r] = pv * (dpv - del);
             }
             // ---- dQ^T += K^T dS^T ----
             if constexpr (C::F32) {

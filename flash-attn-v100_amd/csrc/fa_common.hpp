@@ -287,6 +287,15 @@ __device__ FA_INLINE inline bool philox_keep(uint64_t seed, uint64_t ctr, uint32
     return (uint32_t)(x ^ (x >> 31)) > thresh;
 }
 
+// All ones when bit `pos` of x is set, else zero (one sign-extending
+// bit-field extract); keep_or_zero(v, m) is v where m is all ones, +0 else.
+__device__ FA_INLINE inline uint32_t bit_mask(uint32_t x, int pos) {
+    return (uint32_t)((int32_t)(x << (31 - pos)) >> 31);
+}
+__device__ FA_INLINE inline float keep_or_zero(float v, uint32_t m) {
+    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) & m);
+}
+
 __device__ FA_INLINE inline float philox_uniform(uint64_t seed, uint64_t ctr) {
     int32_t x = (int32_t)philox_word0(seed, ctr);
     x = x < 0 ? -x - 1 : x;
