@@ -232,6 +232,11 @@ int32_t fa_fwd(const fa_fwd_args* a, void* stream) {
     const bool causal = a->causal != 0;
     const bool dropout = a->dropout_p > 0.f;
     hipStream_t s = (hipStream_t)stream;
+    // keep bits requested: draw them first, the forward then reads them
+    if (p.kb) {
+        const int32_t st = status_of(fa::launch_keep_bits(p, causal, s));
+        if (st != FA_OK) return st;
+    }
     if (a->bias) {
         const bool b32 = a->bias_dtype == FA_DTYPE_F32;
         switch (a->dtype) {

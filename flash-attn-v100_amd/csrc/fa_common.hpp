@@ -98,11 +98,6 @@ __device__ FA_INLINE inline float pair_sum(float x) {
     pair_swap(x, a, b);
     return a + b;
 }
-__device__ FA_INLINE inline uint32_t pair_or(uint32_t x) {
-    float a, b;
-    pair_swap(__builtin_bit_cast(float, x), a, b);
-    return __builtin_bit_cast(uint32_t, a) | __builtin_bit_cast(uint32_t, b);
-}
 
 // x of lane `lane ^ S` (S = 1, 2, 4, 8, 16): DPP moves within rows of 16
 // lanes (quad permutes for 1 and 2; row shifts up / down, one per side, for

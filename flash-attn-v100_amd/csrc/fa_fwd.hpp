@@ -141,8 +141,19 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
         }
     };
 
+    // dropout: the mask drawn here (DROPOUT == 1), or read from the keep bits
+    // written just before this kernel (DROPOUT == 2): the words of this lane's
+    // query row for the 32-key blocks of a tile, loaded a tile ahead
     uint64_t row_ctr = 0;
-    if (DROPOUT) row_ctr = p.offset + ((uint64_t)(b * p.H + h) * (uint64_t)p.Sq + (uint64_t)qi) * (uint64_t)p.Sk;
+    if (DROPOUT == 1) row_ctr = p.offset + ((uint64_t)(b * p.H + h) * (uint64_t)p.Sq + (uint64_t)qi) * (uint64_t)p.Sk;
+    const uint32_t* kbrow = p.kb + (DROPOUT == 2 && qi < p.Sq ? ((int64_t)(b * p.H + h) * p.Sq + qi) * p.kb_w : 0);
+    auto load_kb = [&](int k0, uint32_t (&wd)[NB]) FA_INLINE {
+        if constexpr (DROPOUT == 2) {
+#pragma unroll
+            for (int blk = 0; blk < NB; ++blk)
+                wd[blk] = qi < p.Sq && k0 + 32 * blk < p.Sk ? kbrow[(k0 >> 5) + blk] : 0u;
+        }
+    };
 
     T* Ks0 = smem;
     T* Vs0 = smem + 2 * C::KTILE;
@@ -220,7 +231,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     };
     // P = exp2(S * scale * log2 e - m), row sums, dropout; 16-bit types pack P
     constexpr int NPK = C::F32 ? 1 : BN / 16;
-    auto softmax = [&](f32x16 (&s)[NB], s16x8 (&pk)[NPK], int k0) {
+    auto softmax = [&](f32x16 (&s)[NB], s16x8 (&pk)[NPK], int k0, const uint32_t (&wd)[NB]) {
         float psum = 0.f;
 #pragma unroll
         for (int blk = 0; blk < NB; ++blk)
@@ -232,23 +243,16 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
             }
         l_run += psum;
         if (DROPOUT) {
-            constexpr bool bits_out = DROPOUT == 2;
 #pragma unroll
-            for (int blk = 0; blk < NB; ++blk) {
-                uint32_t mine = 0;  // this lane's keep bits of the 32-key block
+            for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int kk = 8 * (r >> 2) + 4 * hi + (r & 3);
-                    const bool keep = philox_keep(p.seed, row_ctr + (uint64_t)(k0 + 32 * blk + kk), p.keep_thresh);
+                    const bool keep = DROPOUT == 2
+                                          ? ((wd[blk] >> kk) & 1u) != 0u
+                                          : philox_keep(p.seed, row_ctr + (uint64_t)(k0 + 32 * blk + kk), p.keep_thresh);
                     if (!keep) s[blk][r] = 0.f;
-                    if (bits_out) mine |= (uint32_t)keep << kk;
                 }
-                if (bits_out) {
-                    const uint32_t word = pair_or(mine);
-                    const int kw = (k0 >> 5) + blk;
-                    if (hi == 0 && qi < p.Sq && k0 + 32 * blk < p.Sk) p.kb[((int64_t)(b * p.H + h) * p.Sq + qi) * p.kb_w + kw] = word;
-                }
-            }
         }
         if constexpr (!C::F32) {
 #pragma unroll
@@ -306,6 +310,7 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     if (CAUSAL) n_w = min(n_tiles, (qw0 + 31) / BN + 1);
     f32x16 sa[NB], sb[NB];
     s16x8 pk[NPK];
+    uint32_t wa[NB], wb[NB];  // keep words of the current / next tile (DROPOUT == 2)
 
     auto sync_tiles = [&]() {
         wait_vmem();
@@ -319,13 +324,15 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     sync_tiles();
     if (n_w > 0) {
         load_bias(0, std::true_type{});
+        load_kb(0, wa);
         qk(Ks0, sa);
         add_bias(sa);
         if (n_plain == 0) mask(sa, 0);
         update_max(sa);
     }
 
-    auto iter = [&](int j, f32x16 (&sc)[NB], f32x16 (&sn)[NB], auto mask_tag) {
+    auto iter = [&](int j, f32x16 (&sc)[NB], f32x16 (&sn)[NB], const uint32_t (&wc)[NB], uint32_t (&wn)[NB],
+                    auto mask_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
         sync_tiles();
         dma_k(j + 2, j & 1);
@@ -335,9 +342,10 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
         if (act) {
             if (next) {
                 load_bias((j + 1) * BN, mask_tag);
+                load_kb((j + 1) * BN, wn);
                 qk(Ks0 + ((j + 1) & 1) * C::KTILE, sn);
             }
-            softmax(sc, pk, j * BN);
+            softmax(sc, pk, j * BN, wc);
         }
         if (act) pv(Vs0 + (j & 1) * C::VTILE, sc, pk);
         if (act && next) {
@@ -352,20 +360,23 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     const int n_pipe = n_plain - 1;
     int j = 0;
     for (; j + 1 < n_pipe; j += 2) {
-        iter(j, sa, sb, std::false_type{});
-        iter(j + 1, sb, sa, std::false_type{});
+        iter(j, sa, sb, wa, wb, std::false_type{});
+        iter(j + 1, sb, sa, wb, wa, std::false_type{});
     }
     if (j < n_pipe) {
-        iter(j, sa, sb, std::false_type{});
+        iter(j, sa, sb, wa, wb, std::false_type{});
         ++j;
 #pragma unroll
-        for (int blk = 0; blk < NB; ++blk) sa[blk] = sb[blk];
+        for (int blk = 0; blk < NB; ++blk) {
+            sa[blk] = sb[blk];
+            wa[blk] = wb[blk];
+        }
     }
     for (; j + 1 < n_tiles; j += 2) {
-        iter(j, sa, sb, std::true_type{});
-        iter(j + 1, sb, sa, std::true_type{});
+        iter(j, sa, sb, wa, wb, std::true_type{});
+        iter(j + 1, sb, sa, wb, wa, std::true_type{});
     }
-    if (j < n_tiles) iter(j, sa, sb, std::true_type{});
+    if (j < n_tiles) iter(j, sa, sb, wa, wb, std::true_type{});
 
     // ---- epilogue: normalise, LSE, stage O^T through LDS, coalesced store ----
     const float l_tot = pair_sum(l_run);

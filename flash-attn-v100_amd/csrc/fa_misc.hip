@@ -1,5 +1,8 @@
 // Test hooks exposing the device RNG exactly as the attention kernels use it,
-// and the broadcast reduction of the bias gradient.
+// the forward's dropout keep bits, and the broadcast reduction of the bias
+// gradient.
+#include <algorithm>
+
 #include "fa_common.hpp"
 #include "fa_params.hpp"
 
@@ -44,6 +47,52 @@ hipError_t launch_dropout_mask(uint64_t seed, uint64_t offset, int B, int H, int
     if (nb > 0x7fffffff) return hipErrorInvalidValue;
     hipLaunchKernelGGL(dropout_mask_kernel, dim3((unsigned)nb), dim3(256), 0, s, seed, offset, n, keep_threshold(p),
                        keep);
+    return hipGetLastError();
+}
+
+// Dropout keep bits: word w of row r = (b*H + h)*Sq + i holds keep(b, h, i,
+// 32 w + t) at bit t.  A wave takes a chunk of KB_KEYS keys of one row: lane l
+// draws keys 64 u + l of the chunk (u < KB_PER_LANE, independent Philox
+// chains that hide each other's multiply latency), then one ballot per u gives
+// two words, which lanes 0 and 1 store.  Under causal masking, chunks whose
+// keys all follow the query are skipped (the kernels never use those bits).
+constexpr int KB_PER_LANE = 8;
+constexpr int KB_KEYS = 64 * KB_PER_LANE;
+// Rows (fewer than 2^31: B*H*Sq rows of q fit in memory) are spread over the
+// waves with 32-bit index math, one division per row.
+__global__ __launch_bounds__(256) void keep_bits_kernel(uint64_t seed, uint64_t offset, uint32_t thresh,
+                                                        uint32_t* __restrict__ kb, int kb_w, int Sq, int Sk, int rows,
+                                                        int chunks, int causal) {
+    const int lane = threadIdx.x & 63;
+    const int step = gridDim.x * 4;
+    for (int row = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); row < rows; row += step) {
+        const int cend = causal ? min(chunks, (row % Sq) / KB_KEYS + 1) : chunks;
+        const uint64_t rbase = offset + (uint64_t)row * (uint64_t)Sk + (uint64_t)lane;
+        uint32_t* out = kb + (int64_t)row * kb_w;
+        for (int c = 0; c < cend; ++c) {
+            bool keep[KB_PER_LANE];
+#pragma unroll
+            for (int u = 0; u < KB_PER_LANE; ++u)
+                keep[u] = philox_keep(seed, rbase + (uint64_t)(KB_KEYS * c + 64 * u), thresh);
+#pragma unroll
+            for (int u = 0; u < KB_PER_LANE; ++u) {
+                // keys past Sk draw too (their bits are never read)
+                const uint64_t bal = __ballot(keep[u]);
+                const int w = (KB_KEYS / 32) * c + 2 * u + lane;  // lanes 0, 1: keys 64 u .. +31, +32 .. +63
+                if (lane < 2 && w < kb_w) out[w] = lane == 0 ? (uint32_t)bal : (uint32_t)(bal >> 32);
+            }
+        }
+    }
+}
+
+hipError_t launch_keep_bits(const FwdParams& p, bool causal, hipStream_t s) {
+    const int64_t rows = (int64_t)p.B * p.H * p.Sq;
+    const int chunks = (p.Sk + KB_KEYS - 1) / KB_KEYS;
+    if (rows <= 0 || chunks <= 0) return hipSuccess;
+    if (rows > 0x7fffffff) return hipErrorInvalidValue;
+    const int64_t nb = std::min<int64_t>((rows + 3) / 4, 1 << 16);
+    hipLaunchKernelGGL(keep_bits_kernel, dim3((unsigned)nb), dim3(256), 0, s, p.seed, p.offset, p.keep_thresh, p.kb,
+                       p.kb_w, p.Sq, p.Sk, (int)rows, chunks, causal ? 1 : 0);
     return hipGetLastError();
 }
 

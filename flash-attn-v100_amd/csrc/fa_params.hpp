@@ -126,6 +126,10 @@ hipError_t launch_bwd_bias32_f16(const BwdParams& p, int D, bool causal, bool dr
 hipError_t launch_dropout_mask(uint64_t seed, uint64_t offset, int B, int H, int Sq, int Sk, float p,
                                uint8_t* keep, hipStream_t s);
 hipError_t launch_rand(uint64_t seed, const uint64_t* ctr, int64_t n, float* u, hipStream_t s);
+// the forward's dropout keep bits (p.kb, p.kb_w, seed, offset, keep_thresh),
+// for the B*H*Sq rows of p; with causal, words whose keys all follow the query
+// may be left unwritten
+hipError_t launch_keep_bits(const FwdParams& p, bool causal, hipStream_t s);
 hipError_t launch_dbias_reduce(const DbiasReduceParams& r, hipStream_t s);
 
 }  // namespace fa
