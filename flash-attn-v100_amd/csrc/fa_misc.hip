@@ -51,48 +51,62 @@ hipError_t launch_dropout_mask(uint64_t seed, uint64_t offset, int B, int H, int
 }
 
 // Dropout keep bits: word w of row r = (b*H + h)*Sq + i holds keep(b, h, i,
-// 32 w + t) at bit t.  A wave takes a chunk of KB_KEYS keys of one row: lane l
-// draws keys 64 u + l of the chunk (u < KB_PER_LANE, independent Philox
-// chains that hide each other's multiply latency), then one ballot per u gives
-// two words, which lanes 0 and 1 store.  Under causal masking, chunks whose
-// keys all follow the query are skipped (the kernels never use those bits).
-constexpr int KB_PER_LANE = 8;
-constexpr int KB_KEYS = 64 * KB_PER_LANE;
-// Rows (fewer than 2^31: B*H*Sq rows of q fit in memory) are spread over the
-// waves with 32-bit index math, one division per row.
+// 32 w + t) at bit t.  A wave takes KB_ROWS consecutive rows and walks their
+// keys 64 * KB_SETS at a time: lane l draws keys k0 + 64 v + l (v < KB_SETS)
+// of each row (KB_ROWS * KB_SETS independent Philox chains, which hide each
+// other's multiply latency), then one ballot per (row, v) gives two words,
+// which lanes 0 and 1 store.  Under causal masking a group stops after the last
+// key any of its queries sees (the bits of keys past a query's own diagonal
+// are drawn but never read).  Rows (fewer than 2^31: B*H*Sq rows of q fit in
+// memory) use 32-bit index math.
+// 2 rows x 4 key groups: measured against 1 x 8, 4 x 2 and 8 x 1, the best
+// balance between long rows (fewer groups per key) and short causal rows
+// (less drawn past the diagonal)
+constexpr int KB_ROWS = 2;
+constexpr int KB_SETS = 8 / KB_ROWS;
 __global__ __launch_bounds__(256) void keep_bits_kernel(uint64_t seed, uint64_t offset, uint32_t thresh,
                                                         uint32_t* __restrict__ kb, int kb_w, int Sq, int Sk, int rows,
-                                                        int chunks, int causal) {
+                                                        int causal) {
     const int lane = threadIdx.x & 63;
+    const int ngroups = (rows + KB_ROWS - 1) / KB_ROWS;
     const int step = gridDim.x * 4;
-    for (int row = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); row < rows; row += step) {
-        const int cend = causal ? min(chunks, (row % Sq) / KB_KEYS + 1) : chunks;
-        const uint64_t rbase = offset + (uint64_t)row * (uint64_t)Sk + (uint64_t)lane;
-        uint32_t* out = kb + (int64_t)row * kb_w;
-        for (int c = 0; c < cend; ++c) {
-            bool keep[KB_PER_LANE];
+    for (int grp = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); grp < ngroups; grp += step) {
+        const int r0 = grp * KB_ROWS;
+        int kend = Sk;
+        if (causal) {  // largest query index among the group's rows
+            const int i0 = r0 % Sq, last = min(KB_ROWS, rows - r0) - 1;
+            kend = min(Sk, (i0 + last < Sq ? i0 + last : Sq - 1) + 1);
+        }
+        for (int k0 = 0; k0 < kend; k0 += 64 * KB_SETS) {
+            bool keep[KB_ROWS][KB_SETS];
 #pragma unroll
-            for (int u = 0; u < KB_PER_LANE; ++u)
-                keep[u] = philox_keep(seed, rbase + (uint64_t)(KB_KEYS * c + 64 * u), thresh);
+            for (int u = 0; u < KB_ROWS; ++u)
 #pragma unroll
-            for (int u = 0; u < KB_PER_LANE; ++u) {
-                // keys past Sk draw too (their bits are never read)
-                const uint64_t bal = __ballot(keep[u]);
-                const int w = (KB_KEYS / 32) * c + 2 * u + lane;  // lanes 0, 1: keys 64 u .. +31, +32 .. +63
-                if (lane < 2 && w < kb_w) out[w] = lane == 0 ? (uint32_t)bal : (uint32_t)(bal >> 32);
-            }
+                for (int v = 0; v < KB_SETS; ++v)
+                    keep[u][v] = philox_keep(
+                        seed, offset + (uint64_t)(r0 + u) * (uint64_t)Sk + (uint64_t)(k0 + 64 * v + lane), thresh);
+#pragma unroll
+            for (int u = 0; u < KB_ROWS; ++u)
+#pragma unroll
+                for (int v = 0; v < KB_SETS; ++v) {
+                    // keys past Sk and rows past the last one draw too (never stored or read)
+                    const uint64_t bal = __ballot(keep[u][v]);
+                    const int w = ((k0 + 64 * v) >> 5) + lane;  // lanes 0, 1: the two 32-key words
+                    if (lane < 2 && w < kb_w && r0 + u < rows)
+                        kb[(int64_t)(r0 + u) * kb_w + w] = lane == 0 ? (uint32_t)bal : (uint32_t)(bal >> 32);
+                }
         }
     }
 }
 
 hipError_t launch_keep_bits(const FwdParams& p, bool causal, hipStream_t s) {
     const int64_t rows = (int64_t)p.B * p.H * p.Sq;
-    const int chunks = (p.Sk + KB_KEYS - 1) / KB_KEYS;
-    if (rows <= 0 || chunks <= 0) return hipSuccess;
-    if (rows > 0x7fffffff) return hipErrorInvalidValue;
-    const int64_t nb = std::min<int64_t>((rows + 3) / 4, 1 << 16);
+    if (rows <= 0 || p.Sk <= 0) return hipSuccess;
+    if (rows > 0x7fffffff - KB_ROWS) return hipErrorInvalidValue;
+    const int64_t groups = (rows + KB_ROWS - 1) / KB_ROWS;
+    const int64_t nb = std::min<int64_t>((groups + 3) / 4, 1 << 16);
     hipLaunchKernelGGL(keep_bits_kernel, dim3((unsigned)nb), dim3(256), 0, s, p.seed, p.offset, p.keep_thresh, p.kb,
-                       p.kb_w, p.Sq, p.Sk, (int)rows, chunks, causal ? 1 : 0);
+                       p.kb_w, p.Sq, p.Sk, (int)rows, causal ? 1 : 0);
     return hipGetLastError();
 }
 
