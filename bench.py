@@ -1,6 +1,7 @@
 """Benchmark of the FlashAttention hot path on one MI355X.
 
-Workload (the headline): B=4, S=4096, H=32, D=128,
+Workload (benchmark config C3, configs[2] of the benchmark definition, the
+headline): B=4, S=4096, H=32, D=128,
 bf16, causal, dropout 0; q, k, v, dO ~ N(0, 1) from torch.Generator('cpu')
 seed 42.  One step = forward + backward through the C ABI (fa_fwd, fa_bwd)
 with inputs resident in HBM.  Algorithmic FLOPs: F_fwd = 4*B*H*S*S*D/2,
@@ -19,7 +20,7 @@ from the dK/dV kernel, accumulated in fp32; for ``heads`` its sum over the batch
 done by the library), inside the timed step.
 The FLOP count is the same (the bias adds no matrix products).
 
-With ``--all-configs`` it instead prints one JSON line per BASELINE config
+With ``--all-configs`` it instead prints one JSON line per benchmark config
 (C1-C5: GPU time and TFLOP/s of the config's pass, and the same CPU baseline on
 a bounded sample of that config); the dropout configs run the autograd
 default, the forward storing the keep bits that the backward reads.
@@ -164,7 +165,7 @@ def cpu_baseline(target_s: float = 12.0, bias_kind: str = "none"):
             "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count()}
 
 
-# name, (B, S, H, D), dtype, causal, dropout p, with backward
+# benchmark configs C1-C5: name, (B, S, H, D), dtype, causal, dropout p, with backward
 ALL_CONFIGS = [
     ("C1", (2, 1024, 12, 64), "float16", False, 0.0, False),
     ("C2", (2, 1024, 12, 64), "float16", True, 0.0, True),
@@ -176,7 +177,7 @@ ALL_CONFIGS = [
 
 
 def all_configs(n: int, cpu: bool, cpu_target_s: float = 3.0, only=None):
-    """One JSON line per BASELINE config: GPU time of its pass (HIP events,
+    """One JSON line per benchmark config: GPU time of its pass (HIP events,
     mean of ``n`` calls) and, unless ``cpu`` is False, the fp32 math path of
     oracle/ on this host for B=1 and as many heads as fit ``cpu_target_s``."""
     import ctypes
@@ -325,7 +326,7 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--all-configs", action="store_true",
-                    help="one JSON line per BASELINE config (C1-C5) instead of the headline line")
+                    help="one JSON line per benchmark config (C1-C5) instead of the headline line")
     ap.add_argument("--config", action="append", choices=[c[0] for c in ALL_CONFIGS],
                     help="with --all-configs: only these configs (repeatable)")
     a = ap.parse_args()

@@ -13,7 +13,7 @@ for p in (REPO, PKG_ROOT):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
-    config.addinivalue_line("markers", "slow: long-running (full BASELINE-size configs)")
+    config.addinivalue_line("markers", "slow: long-running (full-size benchmark configs C1-C5)")
 
 
 def _ensure_built():

@@ -1,4 +1,4 @@
-"""Shared test helpers: BASELINE input recipe, the C oracle library, the
+"""Shared test helpers: the benchmark input recipe, the C oracle library, the
 low-precision error envelope and chunked float64 references."""
 from __future__ import annotations
 
@@ -43,7 +43,7 @@ def c_rand(seed, counters) -> np.ndarray:
 
 
 def make_inputs(B, Sq, H, D, dtype, Sk=None, Hkv=None, seed=42, qk_scale=1.0, device="cpu"):
-    """BASELINE recipe: torch.Generator('cpu').manual_seed(seed), randn fp32 in
+    """Benchmark input recipe: torch.Generator('cpu').manual_seed(seed), randn fp32 in
     the order q, k, v, dO, q/k optionally scaled, cast to ``dtype``."""
     Sk = Sq if Sk is None else Sk
     Hkv = H if Hkv is None else Hkv

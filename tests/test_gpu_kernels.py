@@ -1,9 +1,9 @@
 """Parity of the gfx950 kernels, called through the C ABI, against the oracle.
 
-Tolerance (BASELINE north star): fp16/bf16 outputs within 2x the error of the
+Tolerance: fp16/bf16 outputs within 2x the error of the
 reference's own math run in the same dtype on the GPU (both against the
 float64 oracle); fp32 within 1e-5 of max|oracle|; dropout masks bit-exact.
-Small shapes use the CPU oracle; the BASELINE-size configs evaluate the same
+Small shapes use the CPU oracle; the benchmark configurations C1-C5 evaluate the same
 oracle functions in float64 on the GPU, one head chunk at a time.
 """
 import json
@@ -109,7 +109,7 @@ def test_small_dropout(D):
         assert_parity(res, dt, f"dropout D={D} {dt}")
 
 
-# ----------------------------------------------------------------------------- BASELINE configs
+# ----------------------------------------------------------------------------- benchmark configs C1-C5
 
 def test_c1_forward():
     say("case: C1 (2,1024,12,64) fp16 non-causal fwd")
