@@ -106,7 +106,8 @@ struct DkdvCfg {
 
 // TB: element type of the additive bias (T or float), void = no bias
 template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
-__global__ __launch_bounds__(256, (std::is_void<TB>::value ? 2 : 1)) void dkdv_kernel(const BwdParams p, const int n_ktiles) {
+__global__ __launch_bounds__(256, (std::is_void<TB>::value && !(Elem<T>::kF32 && D == 128) ? 2 : 1)) void dkdv_kernel(
+    const BwdParams p, const int n_ktiles) {
     using C = DkdvCfg<T, D>;
     constexpr bool BIAS = !std::is_void<TB>::value;
     using BT = typename std::conditional<BIAS, TB, T>::type;
