@@ -78,6 +78,8 @@ SMALL += [
     (torch.bfloat16, 1, 1, 1, 2, 2, 64, True),        # single query / key
     (torch.float16, 3, 1, 50, 2, 2, 32, False),       # decode-like
     (torch.bfloat16, 1, 64, 1, 2, 2, 128, False),     # single key
+    (torch.bfloat16, 2, 3, 8192, 4, 1, 128, False),   # decode against a long context (MQA)
+    (torch.float16, 32, 64, 64, 16, 16, 64, True),    # many small (batch, head) slices
 ]
 
 
