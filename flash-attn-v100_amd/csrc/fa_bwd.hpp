@@ -35,7 +35,8 @@ namespace fa {
 // ---------------------------------------------------------------------------
 // delta = rowsum(dO * O) and LSE * log2(e) into the padded workspace rows;
 // padding rows (Sq <= i < sq_pad) get delta = 0 and LSE * log2(e) = +inf, so
-// a query tile that reads them gets P = 0 without a range check.
+// a query tile that reads them gets P = 0 without a range check; so do rows
+// whose saved LSE is -inf.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void delta_kernel(const BwdParams p) {
     constexpr int EPC = 16 / sizeof(T);
@@ -73,7 +74,11 @@ __global__ __launch_bounds__(256) void delta_kernel(const BwdParams p) {
     if (row < nrows && part == 0) {
         const int64_t wi = ((int64_t)b * p.H + h) * p.ws_stride + i;
         p.delta[wi] = acc;
-        p.lse2[wi] = i < p.Sq ? p.lse[((int64_t)b * p.H + h) * p.Sq + i] * kLog2e : INFINITY;
+        // a row with no visible key (every score -inf, e.g. a fully masked bias
+        // row) has LSE = -inf and O = 0: +inf here makes its P = 0, so its
+        // gradients are 0 instead of NaN
+        const float l = i < p.Sq ? p.lse[((int64_t)b * p.H + h) * p.Sq + i] : -INFINITY;
+        p.lse2[wi] = l == -INFINITY ? INFINITY : l * kLog2e;
     }
 }
 
@@ -600,7 +605,7 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
             }
             // the forward's keep bits of this lane's query for the sub-step's keys
             uint32_t kword = 0;
-            if (DROPOUT == 2 && qi < p.Sq)
+            if (DROPOUT == 2 && qi < p.Sq && k0 < p.Sk)
                 kword = p.kb[((int64_t)(b * p.H + h) * p.Sq + qi) * p.kb_w + (k0 >> 5)];
             // ---- S^T = K Q^T, dP^T = V dO^T (C[key][query]) ----
             f32x16 s = f32x16{}, dp = f32x16{};

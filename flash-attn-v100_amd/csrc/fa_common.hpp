@@ -349,7 +349,8 @@ __device__ FA_INLINE inline void dma_load16(__amdgpu_buffer_rsrc_t rs, T* lds, i
 // rows of W elements (W - D of padding).  One wave instruction writes 64
 // consecutive 16-byte LDS chunks, lane l to chunk l (checked on gfx950), so
 // LDS chunk c of the tile is row c / CW, column chunk c % CW (CW = W * size /
-// 16); padding chunks load a copy of the row's last data chunk.  Instructions
+// 16); padding chunks get an out-of-range offset (they read nothing and land
+// as zeros).  Instructions
 // are dealt round-robin to the NW waves of the workgroup.  Rows >= nvalid are
 // outside the buffer range and land as zeros.  The data is in LDS once the
 // issuing wave's vmcnt reaches zero; a workgroup barrier after that wait

@@ -26,7 +26,8 @@
  * it instead of regenerating the Philox stream (same mask, same results).
  * keep_bits: 4-byte aligned uint32 words, row ((b*H + h)*Sq + i) of
  * ceil(Sk/32) words, bit j%32 of word j/32 = keep(b, h, i, j); words whose 32
- * keys causal masking removes for query i are left unwritten (and unread).
+ * keys causal masking removes for query i are left unwritten (the kernels may
+ * read them, but their bits never affect a result).
  */
 #ifndef FA_ABI_H
 #define FA_ABI_H

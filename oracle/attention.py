@@ -51,14 +51,7 @@ __all__ = [
     "attention_autograd",
     "brute_force_forward",
     "reduce_to_bias_shape",
-    "flops",
 ]
-
-
-def flops(B: int, H: int, Sq: int, Sk: int, D: int, causal: bool, bwd: bool = False) -> float:
-    """Algorithmic FLOPs: 4*B*H*Sq*Sk*D*(1/2 if causal); fwd+bwd = 3.5x that."""
-    f = 4.0 * B * H * Sq * Sk * D * (0.5 if causal else 1.0)
-    return f * 3.5 if bwd else f
 
 
 def expand_kv(x: torch.Tensor, num_heads: int) -> torch.Tensor:
@@ -102,8 +95,9 @@ def attention_forward(
 
     ``dropout_mask`` is a bool keep-mask (B, H, Sq, Sk) or None; ``bias`` an
     additive (B|1, H|1, Sq|1, Sk) tensor or None.
-    Rows with no unmasked key (only possible when Sk == 0) give O = 0 and
-    LSE = -inf.
+    Rows with no visible key (Sk == 0, or a bias that is -inf on every key
+    the causal mask leaves) give O = 0, LSE = -inf and zero gradients, as
+    FlashAttention-2 does; the reference's ``softmax`` would give NaN there.
     """
     B, Sq, H, D = q.shape
     if scale is None:
@@ -115,8 +109,16 @@ def attention_forward(
         return (torch.zeros(B, Sq, H, D, dtype=dtype, device=q.device),
                 torch.full((B, H, Sq), float("-inf"), dtype=dtype, device=q.device))
     s = _scores(q, k, causal, scale, dtype, bias)
-    lse = torch.logsumexp(s, dim=-1)
-    p = torch.exp(s - lse.unsqueeze(-1))
+    # softmax through the row max, with rows that see no key (max = -inf)
+    # shifted by 0 instead: their probabilities are then exp(-inf) = 0 and no
+    # -inf - (-inf) = NaN reaches the values or the autograd graph
+    m = s.amax(dim=-1, keepdim=True)
+    dead = torch.isneginf(m)
+    m = torch.where(dead, torch.zeros_like(m), m).detach()
+    e = torch.exp(s - m)
+    tot = e.sum(dim=-1, keepdim=True)
+    lse = (m + torch.log(tot)).squeeze(-1)
+    p = e / torch.where(dead, torch.ones_like(tot), tot)
     if dropout_p > 0.0:
         if dropout_mask is None:
             raise ValueError("dropout_p > 0 needs an explicit keep mask")
@@ -144,7 +146,10 @@ def attention_backward(
     ke = expand_kv(k, H)
     ve = expand_kv(v, H)
     s = _scores(q, ke, causal, scale, dtype, bias)
-    p = torch.exp(s - lse.to(dtype).unsqueeze(-1))  # (B, H, Sq, Sk)
+    # rows with LSE = -inf saw no key: P = 0 there (exp(s - inf))
+    lse_d = lse.to(dtype)
+    lse_d = torch.where(torch.isneginf(lse_d), torch.full_like(lse_d, float("inf")), lse_d)
+    p = torch.exp(s - lse_d.unsqueeze(-1))  # (B, H, Sq, Sk)
     if causal:
         p = p.masked_fill(_causal_mask(Sq, ke.shape[1], p.device), 0.0)
     qh = q.to(dtype).transpose(1, 2)
@@ -232,6 +237,8 @@ def brute_force_forward(q, k, v, causal=False, scale=None, keep=None, dropout_p=
                     bi = i if len(bf[bb][bh]) > 1 else 0
                     sc = {j: x + bf[bb][bh][bi][j] for j, x in sc.items()}
                 m = max(sc.values())
+                if m == float("-inf"):  # no visible key: O = 0, LSE = -inf
+                    continue
                 tot = sum(math.exp(x - m) for x in sc.values())
                 lse[b][h][i] = m + math.log(tot)
                 for j in js:

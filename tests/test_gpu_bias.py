@@ -141,6 +141,42 @@ def test_bias_minus_inf_key_padding():
     assert maxabs(outs[0][:1], o0) < 2e-3 and maxabs(outs[1][:1], l0) < 1e-3
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_bias_row_without_visible_key(causal):
+    # HF-style 4-D masks with padded query rows: a row whose bias is -inf on
+    # every key has O = 0, LSE = -inf, and contributes nothing to the
+    # gradients (dK/dV stay finite; its dQ and dBias rows are 0)
+    B, S, H, D = 2, 150, 2, 64
+    say(f"case: bias row without a visible key causal={causal}")
+    q, k, v, do = make_inputs(B, S, H, D, torch.bfloat16, seed=19)
+    bias = make_bias((B, H, S, S), torch.bfloat16)
+    bias[0, 1, 37, :] = float("-inf")
+    bias[1, 0, 149, :] = float("-inf")
+    outs = run_kernels(q, k, v, do, causal, D ** -0.5, bias)
+    o, lse, dq, dk, dv, db = (t.cpu() for t in outs)
+    for t in (o, dq, dk, dv, db):
+        assert torch.isfinite(t).all()
+    dead = ((0, 1, 37), (1, 0, 149))
+    for b, h, i in dead:
+        assert torch.isneginf(lse[b, h, i]) and not o[b, i, h].any()
+        assert not dq[b, i, h].any() and not db[b, h, i].any()
+    # The rest against the oracle: a dead row adds nothing to dK / dV, which is
+    # what a row with dO = 0 adds, so the reference problem gives the dead rows
+    # a finite bias and dO = 0 (the reference math's softmax would put NaN in
+    # them); the dead rows' own O / LSE entries, checked above, take the
+    # oracle's values so that they do not enter the comparison.
+    bias2, do2 = bias.clone(), do.clone()
+    for b, h, i in dead:
+        bias2[b, h, i] = 0
+        do2[b, i, h] = 0
+    ro, rl = oa.attention_forward(q, k, v, causal, D ** -0.5, bias=bias2)
+    outs2 = [t.double() for t in (o, lse, dq, dk, dv, db)]
+    for b, h, i in dead:
+        outs2[0][b, i, h] = ro[b, i, h]
+        outs2[1][b, h, i] = rl[b, h, i]
+    check(q, k, v, do2, causal, D ** -0.5, bias2, outs2, label="dead row")
+
+
 def test_float32_bias_keeps_precision_with_bf16_inputs():
     # ALiBi-style bias with magnitudes in the hundreds: rounding it to bf16
     # moves logits by up to 0.5, reading it as float32 does not

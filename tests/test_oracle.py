@@ -289,6 +289,34 @@ def test_bias_closed_forms():
     assert torch.allclose(o2, o3, atol=1e-13) and torch.allclose(l2, l3, atol=1e-13)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_bias_row_without_visible_key(causal):
+    # a query row whose bias is -inf on every key: O = 0, LSE = -inf and zero
+    # gradients (FlashAttention-2's convention), the other rows unchanged
+    B, S, H, D = 1, 7, 2, 4
+    q, k, v, do = (_rand((B, S, H, D), s) for s in (171, 172, 173, 174))
+    bias = _rand((1, H, S, S), 175)
+    bias[0, 1, 4, :] = float("-inf")
+    o, lse, dq, dk, dv, db = oa.attention_autograd(q, k, v, do, causal, 0.5, bias=bias)
+    ob, lb = oa.brute_force_forward(q, k, v, causal, 0.5, bias=bias)
+    assert torch.equal(o[0, 4, 1], torch.zeros(D, dtype=torch.float64)) and torch.isneginf(lse[0, 1, 4])
+    assert torch.allclose(o, ob, atol=1e-12, rtol=0) and torch.equal(torch.isneginf(lb), torch.isneginf(lse))
+    fin = ~torch.isneginf(lse)
+    assert torch.allclose(lse[fin], lb[fin], atol=1e-12, rtol=0)
+    for t in (dq, dk, dv, db):
+        assert torch.isfinite(t).all()
+    assert torch.equal(dq[0, 4, 1], torch.zeros(D, dtype=torch.float64))
+    assert torch.equal(db[0, 1, 4], torch.zeros(S, dtype=torch.float64))
+    dq2, dk2, dv2, db2 = oa.attention_backward(q, k, v, o, do, lse, causal, 0.5, bias=bias)
+    for a, b in ((dq, dq2), (dk, dk2), (dv, dv2), (db, db2)):
+        assert torch.allclose(a, b, atol=1e-12, rtol=0)
+    # the remaining rows equal attention with the dead row's query removed
+    # from the problem (rows are independent): compare against head 0, which
+    # has no dead row, run alone
+    o0, l0 = oa.attention_forward(q[:, :, :1], k[:, :, :1], v[:, :, :1], causal, 0.5, bias=bias[:, :1])
+    assert torch.allclose(o[:, :, :1], o0, atol=1e-13) and torch.allclose(lse[:, :1], l0, atol=1e-13)
+
+
 @pytest.mark.parametrize("bshape", BIAS_SHAPES)
 def test_bias_backward_formulas_vs_autograd(bshape):
     B, Sq, Sk, H, Hkv, D = 2, 7, 6, 3, 3, 4
