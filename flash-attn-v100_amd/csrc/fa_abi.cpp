@@ -6,11 +6,47 @@
 
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 
 #include "fa_abi.h"
 #include "fa_params.hpp"
 
+// Device scratch of fa_bwd_static: the backward workspace for callers that
+// cannot allocate.  Each GPU holds its own copy at its own address; host code
+// never passes this name to a kernel or a copy (it is a host-side stand-in),
+// only the address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) unsigned char scratch[FA_BWD_STATIC_SCRATCH_BYTES];
+
 namespace {
+
+// device address of `scratch` per GPU, looked up on the first fa_bwd_static
+// call on that GPU
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// the stream's device (the current one for the null stream); its scratch
+// address, looked up with that device current; nullptr on any HIP error
+void* static_scratch(hipStream_t s) {
+    int dev = -1, cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+    dev = cur;
+    if (s != nullptr) {
+        hipDevice_t d;
+        if (hipStreamGetDevice(s, &d) != hipSuccess) return nullptr;
+        dev = (int)d;
+    }
+    if (dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev]) return g_scratch_ptr[dev];
+    if (dev != cur && hipSetDevice(dev) != hipSuccess) return nullptr;
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (dev != cur) (void)hipSetDevice(cur);
+    if (e != hipSuccess || ptr == nullptr) return nullptr;
+    g_scratch_ptr[dev] = ptr;
+    return ptr;
+}
 
 int elem_size(int32_t dtype) { return dtype == FA_DTYPE_F32 ? 4 : 2; }
 
@@ -166,6 +202,9 @@ const char* fa_strerror(int32_t code) {
             return "bias needs the input dtype or float32, j stride 1, b/h/i strides multiples of 16 bytes and a "
                    "16-byte aligned base; dbias needs a bias, dtype fp16/bf16/fp32, j stride 1, i stride >= Sk "
                    "and an aligned base";
+        case FA_ERR_SCRATCH:
+            return "the backward needs more workspace than the static scratch of fa_bwd_static "
+                   "(FA_BWD_STATIC_SCRATCH_BYTES); use fa_bwd with a workspace";
         default: return "unknown status code";
     }
 }
@@ -416,6 +455,20 @@ int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int
 
 int32_t fa_bwd(const fa_bwd_args* a, void* workspace, size_t ws_bytes, void* stream) {
     return fa_bwd_stage(a, workspace, ws_bytes, -1, stream);
+}
+
+int32_t fa_bwd_static(const fa_bwd_args* a, void* stream) {
+    // everything that can be rejected is rejected before any HIP call
+    int32_t st = fa_bwd_check(a, FA_BWD_STATIC_SCRATCH_BYTES);
+    if (st == FA_ERR_WORKSPACE) return FA_ERR_SCRATCH;
+    if (st) return st;
+    if (fa_bwd_workspace_size(a) > FA_BWD_STATIC_SCRATCH_BYTES) return FA_ERR_SCRATCH;
+    if ((int64_t)a->batch * a->num_heads * a->seqlen_q == 0 &&
+        (int64_t)a->batch * a->num_heads_kv * a->seqlen_k == 0)
+        return FA_OK;
+    void* ws = static_scratch((hipStream_t)stream);
+    if (!ws) return FA_ERR_LAUNCH;
+    return fa_bwd_stage(a, ws, FA_BWD_STATIC_SCRATCH_BYTES, -1, stream);
 }
 
 int32_t fa_dropout_mask(uint64_t seed, uint64_t offset, int32_t B, int32_t H, int32_t Sq, int32_t Sk,

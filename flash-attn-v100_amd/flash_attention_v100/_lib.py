@@ -73,8 +73,12 @@ class BwdArgs(ctypes.Structure):
 
 EXPORTS = (
     "fa_abi_version", "fa_strerror", "fa_fwd_check", "fa_fwd", "fa_bwd_workspace_size",
-    "fa_bwd_check", "fa_bwd", "fa_bwd_stage", "fa_dropout_mask", "fa_rand",
+    "fa_bwd_check", "fa_bwd", "fa_bwd_stage", "fa_bwd_static", "fa_dropout_mask", "fa_rand",
 )
+
+# device scratch of fa_bwd_static (FA_BWD_STATIC_SCRATCH_BYTES in fa_abi.h)
+BWD_STATIC_SCRATCH_BYTES = 32 << 20
+ERR_SCRATCH = -14
 
 _lib = None
 
@@ -109,6 +113,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.fa_bwd.argtypes = [P(BwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     lib.fa_bwd_stage.restype = ctypes.c_int32
     lib.fa_bwd_stage.argtypes = [P(BwdArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_void_p]
+    lib.fa_bwd_static.restype = ctypes.c_int32
+    lib.fa_bwd_static.argtypes = [P(BwdArgs), ctypes.c_void_p]
     lib.fa_dropout_mask.restype = ctypes.c_int32
     lib.fa_dropout_mask.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int32, ctypes.c_int32,
                                     ctypes.c_int32, ctypes.c_int32, ctypes.c_float, ctypes.c_void_p,
@@ -340,6 +346,24 @@ def bwd(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float = 0.0,
     _check("fa_bwd", lib.fa_bwd(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(q)))
     if want_dbias:
         return dq, dk, dv, reduce_dbias(dbias, pb)
+    return dq, dk, dv
+
+
+def bwd_static(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float = 0.0,
+               seed: int = 0, offset: int = 0, keep_bits: Optional[torch.Tensor] = None):
+    """Run ``fa_bwd_static`` (the backward on the library's own device
+    scratch, no workspace): returns (dq, dk, dv).  Outputs are allocated here
+    by torch; the library call itself allocates nothing."""
+    lib = load()
+    q, k, v, o, do = (prepare(t) for t in (q, k, v, o, do))
+    lse = lse.contiguous()
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    if keep_bits is not None:
+        _check_keep_bits(keep_bits, q.shape[0], q.shape[2], q.shape[1], k.shape[1], q.device)
+    a = bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, offset, None, None, keep_bits)
+    _check("fa_bwd_static", lib.fa_bwd_static(ctypes.byref(a), _stream(q)))
     return dq, dk, dv
 
 

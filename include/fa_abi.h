@@ -64,6 +64,12 @@ extern "C" {
                                  bytes (S = its sequence length), or Sq + 256 rows
                                  of a bias / dbias slice do */
 #define FA_ERR_BIAS -13       /* bias / dbias dtype, strides or alignment violate the rules above */
+#define FA_ERR_SCRATCH -14    /* fa_bwd_static: the problem needs more workspace than
+                                 FA_BWD_STATIC_SCRATCH_BYTES */
+
+/* Size of the device scratch fa_bwd_static uses instead of a workspace
+ * argument (one copy per GPU, held until the process ends). */
+#define FA_BWD_STATIC_SCRATCH_BYTES (32u << 20)
 
 /* Forward arguments.
  * Replaces the launcher flash_attention_forward_triton_enhanced
@@ -197,6 +203,22 @@ int32_t fa_bwd(const fa_bwd_args* args, void* workspace, size_t workspace_bytes,
  * fused Triton backward, kernels/backward_kernel.py:17-205). */
 int32_t fa_bwd_stage(const fa_bwd_args* args, void* workspace, size_t workspace_bytes, int32_t stage,
                      void* hip_stream);
+
+/* fa_bwd without a workspace argument and without any allocation: the
+ * workspace is the library's own device scratch array of
+ * FA_BWD_STATIC_SCRATCH_BYTES on the stream's GPU.  Same kernels and results
+ * as fa_bwd.  Returns FA_ERR_SCRATCH when fa_bwd_workspace_size(args) exceeds
+ * the scratch (B * H * Sq rows up to about 4M, fewer with a summed dbias).
+ * Every call on one GPU shares that GPU's scratch: calls that overlap on one
+ * GPU (on different streams, or from different threads) race, so a caller
+ * serialises them (one stream, or its own ordering).  No scratch contents carry
+ * over between calls: stage 0 writes every workspace row the later stages read.
+ * The first call on a GPU looks the array's device address up once
+ * (hipGetSymbolAddress).
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). */
+int32_t fa_bwd_static(const fa_bwd_args* args, void* hip_stream);
 
 /* Test hook: the dropout keep mask the kernels apply, keep[b][h][i][j] =
  * U(seed, offset + ((b*H + h)*Sq + i)*Sk + j) > p, as uint8 (B, H, Sq, Sk),

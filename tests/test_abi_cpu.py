@@ -199,6 +199,33 @@ def test_bwd_workspace_and_checks():
     assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_ERR_NULL_ARG"]
 
 
+def test_bwd_static_rejects_problems_beyond_its_scratch():
+    # fa_bwd_static validates like fa_bwd and refuses, before any device call,
+    # a problem whose workspace exceeds FA_BWD_STATIC_SCRATCH_BYTES
+    lib = _lib.load()
+    text = open(HEADER).read()
+    assert re.search(r"#define FA_BWD_STATIC_SCRATCH_BYTES \(32u << 20\)", text)
+    assert _lib.BWD_STATIC_SCRATCH_BYTES == 32 << 20 and _lib.ERR_SCRATCH == CODES["FA_ERR_SCRATCH"]
+    q = torch.zeros(1, 8, 64, 64, dtype=torch.bfloat16)
+    lse = torch.zeros(1, 64, 8)
+    a = _lib.bwd_args(q, q, q, q, q, lse, q, q, q, True, 0.125, 0.0, 0, 0)
+    for S, want in ((70000, "FA_ERR_SCRATCH"), (65537, "FA_ERR_SCRATCH")):
+        a.seqlen_q = a.seqlen_k = S
+        ws = lib.fa_bwd_workspace_size(ctypes.byref(a))
+        assert ws > _lib.BWD_STATIC_SCRATCH_BYTES
+        assert lib.fa_bwd_static(ctypes.byref(a), None) == CODES[want]
+    # exactly at the limit the size check passes (64 heads x 65536 rows x 2 x 4 bytes)
+    a.seqlen_q = a.seqlen_k = 65536
+    assert lib.fa_bwd_workspace_size(ctypes.byref(a)) == _lib.BWD_STATIC_SCRATCH_BYTES
+    # argument errors keep their own codes
+    a.dropout_p = 2.0
+    assert lib.fa_bwd_static(ctypes.byref(a), None) == CODES["FA_ERR_DROPOUT"]
+    a.dropout_p = 0.0
+    a.dq = None
+    assert lib.fa_bwd_static(ctypes.byref(a), None) == CODES["FA_ERR_NULL_ARG"]
+    assert lib.fa_strerror(CODES["FA_ERR_SCRATCH"]).decode().startswith("the backward needs more workspace")
+
+
 def test_rng_hooks_validation():
     lib = _lib.load()
     assert lib.fa_dropout_mask(1, 0, 1, 1, 4, 4, 1.5, None, None) == CODES["FA_ERR_DROPOUT"]
