@@ -71,6 +71,9 @@ int32_t check_common(int32_t B, int32_t Sq, int32_t Sk, int32_t H, int32_t Hkv, 
     // grid sizes: (ceil(S / 32) tiles) x heads x batch must fit a 32-bit grid
     const int64_t tiles = ((int64_t)(Sq > Sk ? Sq : Sk) + 31) / 32;
     if (tiles * (int64_t)H * (int64_t)B > 0x7fffffffLL) return FA_ERR_TOO_LARGE;
+    // byte offsets within one row of the backward workspace (2 * Sq floats)
+    // and of the keep bits stay 32-bit
+    if (Sq >= (1 << 28) || Sk >= (1 << 28)) return FA_ERR_TOO_LARGE;
     return FA_OK;
 }
 
@@ -82,19 +85,16 @@ void split(const int64_t st[4], int64_t& sb, int64_t& ss, int64_t& sh) {
 
 int32_t status_of(hipError_t e) { return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH; }
 
-// The kernels address one (batch, head) slice of a tensor through a raw buffer
-// descriptor with a 32-bit byte range: rows [0, S) of the slice must span
-// less than 2^31 bytes.
-// Kernels address one (batch, head) slice through a 32-bit buffer range and
-// compute tile offsets for up to kTileRows rows past a tile's first row (rows
-// past the sequence are zero-filled by the range check), so the byte span of
-// max(S, kTileRows) rows must fit 31 bits.
+// The kernels copy tiles of a (batch, head) slice through a buffer descriptor
+// rebuilt per tile, whose 32-bit byte range covers at most the tile's rows;
+// lanes address up to kTileRows rows past a tile's first row (padding chunks
+// sit past the range), so the byte span of kTileRows rows must stay below
+// 2^31.  The length of the whole slice is not limited.
 constexpr int32_t kTileRows = 256;
 
 int32_t check_span(const int64_t st[4], int32_t S, int32_t D, int es) {
     if (S <= 0) return FA_OK;
-    const int64_t rows = S > kTileRows ? S : kTileRows;
-    const int64_t span = ((rows - 1) * st[1] + D) * es;
+    const int64_t span = ((int64_t)(kTileRows - 1) * st[1] + D) * es;
     return span < (1LL << 31) ? FA_OK : FA_ERR_TOO_LARGE;
 }
 

@@ -309,18 +309,18 @@ __device__ FA_INLINE inline int xcd_remap(int L, int N) {
 }
 
 // ---------------------------------------------------------------------------
-// Raw buffer view of rows [0, nvalid) of a row-strided [rows][D] slice: loads
-// at byte offsets past the last valid row return zeros (hardware range check),
-// which zero-fills tail tiles without any per-lane branch or select.  The
-// descriptor is rebuilt per tile (base advanced, record count reduced) so the
-// range check never depends on the scalar offset.
-//
-// The host rejects slices whose rows span 2^31 bytes or more, so for
-// 0 <= nvalid <= rows the byte count fits 32 bits; it is computed without a
-// branch (nvalid <= 0 gives 0) so that a tile load does not end a basic block.
-template <typename T, int D>
+// Raw buffer view of the rows [0, min(nvalid, R)) of a tile of R rows in a
+// row-strided [rows][D] slice: loads at byte offsets past the last valid row
+// return zeros (hardware range check), which zero-fills tail tiles without any
+// per-lane branch or select.  The descriptor is rebuilt per tile (base
+// advanced to the tile, record count bounded by the tile's rows), so the range
+// check never depends on the scalar offset and only tile-local offsets need 32
+// bits: the host bounds the byte span of kTileRows rows below 2^31, whatever
+// the length of the whole slice.  The byte count is computed without a branch
+// (nvalid <= 0 gives 0) so that a tile load does not end a basic block.
+template <typename T, int D, int R>
 __device__ FA_INLINE inline __amdgpu_buffer_rsrc_t row_buffer(const T* base, int64_t row_stride, int nvalid) {
-    const int nv = max(nvalid, 0);
+    const int nv = min(max(nvalid, 0), R);
     const int bytes = ((nv - 1) * (int)row_stride + D) * (int)sizeof(T) * min(nv, 1);
     // dword 3: DATA_FORMAT = 32 (untyped dword access), no swizzle, no stride
     return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
@@ -380,7 +380,7 @@ struct DmaTile {
         }
     }
     __device__ FA_INLINE inline void load(const T* base, int64_t row_stride, int nvalid, T* lds, int lane) const {
-        const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D>(base, row_stride, nvalid);
+        const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D, R>(base, row_stride, nvalid);
 #pragma unroll
         for (int t = 0; t < PER; ++t) {
             const int g = wave + NW * t;
@@ -389,42 +389,6 @@ struct DmaTile {
                     dma_load16(rs, lds + 64 * g * EPC, off[t]);
             }
         }
-    }
-};
-
-// Branch-free variant for software-pipelined loops: the tile is copied by
-// NWAVES waves with the same number of whole instructions each; the spare
-// lanes of the last instructions copy rows past R into slack space that the
-// caller allocates (LDS_BYTES per tile).  No per-lane or per-wave branch, so
-// the copies can be scheduled between MFMAs.
-template <typename T, int R, int D, int W, int NWAVES>
-struct DmaRows {
-    static constexpr int EPC = 16 / (int)sizeof(T);
-    static constexpr int CD = D / EPC;
-    static constexpr int CW = W / EPC;
-    static_assert(D % EPC == 0 && W % EPC == 0 && W >= D, "16-byte chunked rows");
-    static constexpr int NI = ((R * CW + 63) / 64 + NWAVES - 1) / NWAVES * NWAVES;
-    static constexpr int PER = NI / NWAVES;
-    static constexpr int LDS_BYTES = NI * 64 * 16;
-    int off[PER];
-    int wave;
-
-    // wave_id: this wave's index among the NWAVES copying waves (wave-uniform)
-    __device__ FA_INLINE inline void init(int64_t row_stride, int lane, int wave_id) {
-        wave = wave_id;
-#pragma unroll
-        for (int t = 0; t < PER; ++t) {
-            const int c = 64 * (wave + NWAVES * t) + lane;
-            const int row = c / CW, col = c % CW;
-            off[t] = col < CD ? (row * (int)row_stride + col * EPC) * (int)sizeof(T) : kOffNowhere;
-        }
-    }
-    // copies this wave's instructions [T0, T1) of the tile
-    template <int T0 = 0, int T1 = PER>
-    __device__ FA_INLINE inline void load(const T* base, int64_t row_stride, int nvalid, T* lds) const {
-        const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D>(base, row_stride, nvalid);
-#pragma unroll
-        for (int t = T0; t < (T1 < PER ? T1 : PER); ++t) dma_load16(rs, lds + 64 * (wave + NWAVES * t) * EPC, off[t]);
     }
 };
 
@@ -451,12 +415,13 @@ struct DmaRowGroups {
         wave = wave_id;
         rowl = lane < KR * CW ? lane / CW : KR;
         // padding chunks read nothing: an offset past the range stays past it
-        // after the group's row step is added (slices span < 2^31 bytes)
+        // (below 2^32) after the group's row step is added (tiles span < 2^31
+        // bytes)
         const int col = lane % CW;
         off = col < CD ? ((lane / CW) * (int)row_stride + col * EPC) * (int)sizeof(T) : kOffNowhere;
     }
     __device__ FA_INLINE inline void load(const T* base, int64_t row_stride, int nvalid, T* lds) const {
-        const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D>(base, row_stride, nvalid);
+        const __amdgpu_buffer_rsrc_t rs = row_buffer<T, D, R>(base, row_stride, nvalid);
 #pragma unroll
         for (int t = 0; t < PER; ++t) {
             const int g = wave + NWAVES * t;

@@ -59,10 +59,9 @@ extern "C" {
 #define FA_ERR_ALIGN -9       /* a tensor base pointer is not 16-byte aligned */
 #define FA_ERR_SCALE -10      /* scale not finite and > 0 */
 #define FA_ERR_LAUNCH -11     /* the HIP runtime rejected a kernel launch */
-#define FA_ERR_TOO_LARGE -12  /* a grid dimension would overflow, or max(S, 256) rows
-                                 of one (batch, head) slice of a tensor span >= 2^31
-                                 bytes (S = its sequence length), or Sq + 256 rows
-                                 of a bias / dbias slice do */
+#define FA_ERR_TOO_LARGE -12  /* a grid dimension would overflow, or 256 rows of a
+                                 tensor (its sequence stride times 256) span >= 2^31
+                                 bytes, or Sq + 256 rows of a bias / dbias slice do */
 #define FA_ERR_BIAS -13       /* bias / dbias dtype, strides or alignment violate the rules above */
 #define FA_ERR_SCRATCH -14    /* fa_bwd_static: the problem needs more workspace than
                                  FA_BWD_STATIC_SCRATCH_BYTES */

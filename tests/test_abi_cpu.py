@@ -168,11 +168,43 @@ def test_fwd_check_strides_and_alignment():
     assert _status(a) == CODES["FA_ERR_ALIGN"]
 
 
-def test_fwd_check_rejects_slices_beyond_buffer_range():
+def test_fwd_check_accepts_slices_beyond_2_gib():
+    # each tile is copied through a buffer range of its own rows, so a (b, h)
+    # slice may span more than 2^31 bytes: B=1, S=262144, H=64, D=128 bf16
+    # (one slice spans 4 GiB)
+    B, S, H, D = 1, 262144, 64, 128
+    a, _keep = _cpu_fwd(B=1, Sq=4, Sk=4, H=4, Hkv=4, D=D, dtype=torch.bfloat16)
+    a.seqlen_q = a.seqlen_k = S
+    a.num_heads = a.num_heads_kv = H
+    for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        setattr(a, name, _lib._I64x4(S * H * D, H * D, D, 1))
+    assert ((S - 1) * H * D + D) * 2 >= 2 ** 31
+    assert _status(a) == CODES["FA_OK"]
+    # the backward checks the same spans
+    q = torch.zeros(1, 4, 4, D, dtype=torch.bfloat16)
+    lse = torch.zeros(1, 4, 4)
+    b = _lib.bwd_args(q, q, q, q, q, lse, q, q, q, True, D ** -0.5, 0.0, 0, 0)
+    b.seqlen_q = b.seqlen_k = S
+    b.num_heads = b.num_heads_kv = H
+    for name in ("q_stride", "k_stride", "v_stride", "o_stride", "do_stride", "dq_stride", "dk_stride", "dv_stride"):
+        setattr(b, name, _lib._I64x4(S * H * D, H * D, D, 1))
+    ws = _lib.load().fa_bwd_workspace_size(ctypes.byref(b))
+    assert _lib.load().fa_bwd_check(ctypes.byref(b), ws) == CODES["FA_OK"]
+
+
+def test_fwd_check_rejects_tiles_beyond_buffer_range():
+    # 256 rows of a tensor must span less than 2^31 bytes (a tile's buffer range)
     a, _keep = _cpu_fwd()
-    a.seqlen_k = 70000
-    a.k_stride[1] = 64 * 256  # rows of one head 32 KiB apart: 70000 rows span > 2 GiB
-    a.k_stride[0] = a.k_stride[1] * 70000
+    a.seqlen_k = 300
+    a.k_stride[1] = 2 ** 22 + 2 ** 17  # rows 8.25 MiB apart (fp16): 255 row steps exceed 2 GiB
+    a.k_stride[0] = a.k_stride[1] * 300
+    assert _status(a) == CODES["FA_ERR_TOO_LARGE"]
+    a.k_stride[1] = 2 ** 22  # 8 MiB apart: 255 row steps plus one row stay below 2 GiB
+    a.k_stride[0] = a.k_stride[1] * 300
+    assert _status(a) == CODES["FA_OK"]
+    # sequence lengths of 2^28 or more are refused (32-bit workspace offsets)
+    a, _keep = _cpu_fwd()
+    a.seqlen_k = 2 ** 28
     assert _status(a) == CODES["FA_ERR_TOO_LARGE"]
 
 

@@ -196,6 +196,26 @@ def test_strided_inputs_match_contiguous():
         assert torch.equal(x, y)
 
 
+def test_slices_spanning_more_than_2_gib():
+    # q, k, v, dO are one-head views into a (1, 16384, 1024, 128) bf16 buffer:
+    # each (b, h) slice spans 4 GiB, beyond a 32-bit buffer range, while the
+    # work stays that of one head.  The outputs must equal those of contiguous
+    # copies bit for bit (same kernels, same values).
+    S, HB, D = 16384, 1024, 128
+    say(f"case: one head of a (1, {S}, {HB}, {D}) bf16 buffer, causal fwd+bwd")
+    buf = torch.empty(1, S, HB, D, device=DEV, dtype=torch.bfloat16)
+    src = make_inputs(1, S, 1, D, torch.bfloat16, seed=6)
+    for i, t in enumerate(src):
+        buf[:, :, i:i + 1] = t.to(DEV)
+    views = [buf[:, :, i:i + 1] for i in range(4)]
+    assert views[0].stride(1) * (S - 1) * 2 >= 2 ** 31
+    a = run(*views, True, D ** -0.5)
+    b = run(*(t.to(DEV) for t in src), True, D ** -0.5)
+    for name, x, y in zip(("O", "LSE", "dQ", "dK", "dV"), a, b):
+        assert torch.equal(x, y), name
+    del buf, views
+
+
 def test_empty_keys():
     say("case: Sk = 0")
     q = torch.randn(1, 5, 2, 64, device=DEV, dtype=torch.float16)
