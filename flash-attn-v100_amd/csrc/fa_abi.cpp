@@ -17,6 +17,30 @@
 // only the address hipGetSymbolAddress returns for the current device.
 static __device__ __align__(256) unsigned char scratch[FA_BWD_STATIC_SCRATCH_BYTES];
 
+namespace fa {
+
+// Largest fold value x with fp32(x) * 4.6566127342e-10 <= p, by bisection over
+// the same int -> float conversion and fp32 multiply the device performs
+// (u is non-decreasing in x).
+uint32_t keep_threshold(float p) {
+    auto u = [](uint32_t x) {
+        volatile float xf = (float)(int32_t)x;  // the device's int -> float conversion, then one fp32 multiply
+        return xf * 4.6566127342e-10f;
+    };
+    uint32_t lo = 0, hi = 0x7fffffffu;  // u(lo) = 0 <= p; u(hi) ~ 1 > p for p < 1
+    if (!(u(hi) > p)) return hi;
+    while (hi - lo > 1) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (u(mid) <= p)
+            lo = mid;
+        else
+            hi = mid;
+    }
+    return lo;
+}
+
+}  // namespace fa
+
 namespace {
 
 // device address of `scratch` per GPU, looked up on the first fa_bwd_static
@@ -52,11 +76,26 @@ int elem_size(int32_t dtype) { return dtype == FA_DTYPE_F32 ? 4 : 2; }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Strides beyond 2^40 elements (larger than any device memory) are refused
+// before any arithmetic on them, so that the products below stay far from
+// int64 overflow.
+constexpr int64_t kMaxStride = (int64_t)1 << 40;
+
+// a * b for non-negative a, b; -1 when the product exceeds 2^62
+int64_t mul_capped(int64_t a, int64_t b) {
+    int64_t r;
+    if (__builtin_mul_overflow(a, b, &r) || r > ((int64_t)1 << 62)) return -1;
+    return r;
+}
+
 // d stride 1; b, s, h strides non-negative multiples of 16 bytes
 int32_t check_strides(const int64_t st[4], int es) {
     if (st[3] != 1) return FA_ERR_STRIDE;
-    for (int i = 0; i < 3; ++i)
-        if (st[i] < 0 || (st[i] * es) % 16 != 0) return FA_ERR_STRIDE;
+    for (int i = 0; i < 3; ++i) {
+        if (st[i] < 0) return FA_ERR_STRIDE;
+        if (st[i] > kMaxStride) return FA_ERR_TOO_LARGE;
+        if ((st[i] * es) % 16 != 0) return FA_ERR_STRIDE;
+    }
     return FA_OK;
 }
 
@@ -68,12 +107,13 @@ int32_t check_common(int32_t B, int32_t Sq, int32_t Sk, int32_t H, int32_t Hkv, 
     if (H == 0 || Hkv == 0 || H % Hkv != 0) return FA_ERR_HEADS;
     if (!std::isfinite(scale) || !(scale > 0.f)) return FA_ERR_SCALE;
     if (!std::isfinite(dropout_p) || dropout_p < 0.f || dropout_p >= 1.f) return FA_ERR_DROPOUT;
-    // grid sizes: (ceil(S / 32) tiles) x heads x batch must fit a 32-bit grid
-    const int64_t tiles = ((int64_t)(Sq > Sk ? Sq : Sk) + 31) / 32;
-    if (tiles * (int64_t)H * (int64_t)B > 0x7fffffffLL) return FA_ERR_TOO_LARGE;
     // byte offsets within one row of the backward workspace (2 * Sq floats)
     // and of the keep bits stay 32-bit
     if (Sq >= (1 << 28) || Sk >= (1 << 28)) return FA_ERR_TOO_LARGE;
+    // grid sizes: (ceil(S / 32) tiles) x heads x batch must fit a 32-bit grid
+    // (tiles x heads < 2^54; compared against the limit divided by the batch)
+    const int64_t tiles = ((int64_t)(Sq > Sk ? Sq : Sk) + 31) / 32;
+    if (B > 0 && tiles * (int64_t)H > 0x7fffffffLL / B) return FA_ERR_TOO_LARGE;
     return FA_OK;
 }
 
@@ -102,8 +142,10 @@ int32_t check_span(const int64_t st[4], int32_t S, int32_t D, int es) {
 // through a buffer whose 32-bit offsets are (row * i_stride + key) * elem with
 // row < Sq + 256 and key < Sk + 256 (tiles overhang the sequences).
 int32_t check_slice_offsets(const int64_t st[4], int32_t Sq, int32_t Sk, int es) {
+    if (st[2] > kMaxStride) return FA_ERR_TOO_LARGE;
     const int64_t rows = (int64_t)(Sq > 0 ? Sq : 1) + 256;
-    return (rows * st[2] + Sk + 256) * es < (1LL << 31) ? FA_OK : FA_ERR_TOO_LARGE;
+    const int64_t span = mul_capped(rows, st[2]);
+    return span >= 0 && (span + Sk + 256) * es < (1LL << 31) ? FA_OK : FA_ERR_TOO_LARGE;
 }
 
 // bytes of one (batch, head) slice: rows [0, Sq) of Sk keys
@@ -121,8 +163,11 @@ int32_t check_bias(const void* bias, const int64_t st[4], int32_t bias_dtype, in
     if (bias_dtype != dtype && bias_dtype != FA_DTYPE_F32) return FA_ERR_BIAS;
     const int es = elem_size(bias_dtype);
     if (!aligned16(bias) || st[3] != 1) return FA_ERR_BIAS;
-    for (int i = 0; i < 3; ++i)
-        if (st[i] < 0 || (st[i] * es) % 16 != 0) return FA_ERR_BIAS;
+    for (int i = 0; i < 3; ++i) {
+        if (st[i] < 0) return FA_ERR_BIAS;
+        if (st[i] > kMaxStride) return FA_ERR_TOO_LARGE;
+        if ((st[i] * es) % 16 != 0) return FA_ERR_BIAS;
+    }
     return check_slice_offsets(st, Sq, Sk, es);
 }
 
@@ -147,14 +192,21 @@ int32_t check_dbias(const fa_bwd_args* a) {
     if (dt != FA_DTYPE_F16 && dt != FA_DTYPE_BF16 && dt != FA_DTYPE_F32) return FA_ERR_BIAS;
     const int es = elem_size(dt);
     if (((uintptr_t)dbias % (uintptr_t)es) || st[3] != 1 || st[2] < a->seqlen_k) return FA_ERR_BIAS;
-    for (int i = 0; i < 3; ++i)
+    for (int i = 0; i < 3; ++i) {
         if (st[i] < 0) return FA_ERR_BIAS;
+        if (st[i] > kMaxStride) return FA_ERR_TOO_LARGE;
+    }
     if (dbias_reduced(a)) {
         if (!aligned16(dbias)) return FA_ERR_BIAS;
         for (int i = 0; i < 3; ++i)
             if (st[i] % 4 != 0) return FA_ERR_BIAS;
         const int64_t part_st[4] = {0, 0, dbias_part_row(a->seqlen_k), 1};
         if (check_slice_offsets(part_st, a->seqlen_q, a->seqlen_k, 4)) return FA_ERR_TOO_LARGE;
+        // the float32 parts of every (batch, head) must be addressable (and their
+        // workspace size representable)
+        const int64_t parts = mul_capped(mul_capped((int64_t)a->batch * a->num_heads, a->seqlen_q),
+                                         (int64_t)dbias_part_row(a->seqlen_k) * 4);
+        if (parts < 0) return FA_ERR_TOO_LARGE;
     }
     return check_slice_offsets(st, a->seqlen_q, a->seqlen_k, es);
 }
@@ -475,10 +527,11 @@ int32_t fa_dropout_mask(uint64_t seed, uint64_t offset, int32_t B, int32_t H, in
                         float dropout_p, uint8_t* keep, void* stream) {
     if (B < 0 || H < 0 || Sq < 0 || Sk < 0) return FA_ERR_SHAPE;
     if (!std::isfinite(dropout_p) || dropout_p < 0.f || dropout_p >= 1.f) return FA_ERR_DROPOUT;
-    const int64_t n = (int64_t)B * H * Sq * Sk;
+    // element count, capped (-1) before it could overflow
+    const int64_t n = mul_capped(mul_capped((int64_t)B * H, Sq), Sk);
     if (n == 0) return FA_OK;
     if (!keep) return FA_ERR_NULL_ARG;
-    if ((n + 255) / 256 > 0x7fffffffLL) return FA_ERR_TOO_LARGE;
+    if (n < 0 || n > 0x7fffffffLL * 256) return FA_ERR_TOO_LARGE;
     return status_of(fa::launch_dropout_mask(seed, offset, B, H, Sq, Sk, dropout_p, keep, (hipStream_t)stream));
 }
 
@@ -486,7 +539,7 @@ int32_t fa_rand(uint64_t seed, const uint64_t* counters, int64_t n, float* u, vo
     if (n < 0) return FA_ERR_SHAPE;
     if (n == 0) return FA_OK;
     if (!counters || !u) return FA_ERR_NULL_ARG;
-    if ((n + 255) / 256 > 0x7fffffffLL) return FA_ERR_TOO_LARGE;
+    if (n > 0x7fffffffLL * 256) return FA_ERR_TOO_LARGE;
     return status_of(fa::launch_rand(seed, counters, n, u, (hipStream_t)stream));
 }
 

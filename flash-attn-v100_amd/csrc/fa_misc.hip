@@ -14,23 +14,6 @@ __global__ __launch_bounds__(256) void dropout_mask_kernel(uint64_t seed, uint64
     if (i < n) keep[i] = philox_keep(seed, offset + (uint64_t)i, thresh) ? 1 : 0;
 }
 
-uint32_t keep_threshold(float p) {
-    auto u = [](uint32_t x) {
-        volatile float xf = (float)(int32_t)x;  // the device's int -> float conversion, then one fp32 multiply
-        return xf * 4.6566127342e-10f;
-    };
-    uint32_t lo = 0, hi = 0x7fffffffu;  // u(lo) = 0 <= p; u(hi) ~ 1 > p for p < 1
-    if (!(u(hi) > p)) return hi;
-    while (hi - lo > 1) {
-        const uint32_t mid = lo + (hi - lo) / 2;
-        if (u(mid) <= p)
-            lo = mid;
-        else
-            hi = mid;
-    }
-    return lo;
-}
-
 __global__ __launch_bounds__(256) void rand_kernel(uint64_t seed, const uint64_t* __restrict__ ctr, int64_t n,
                                                    float* __restrict__ u) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;

@@ -99,7 +99,7 @@ constexpr int kSqPad = 128;
 
 // Largest fold value x in [0, 2^31) whose uniform fp32(x) * 4.6566127342e-10
 // (round to nearest, as the device computes it) is <= p: a mask element is
-// kept exactly when its fold value exceeds it (host code, fa_misc.hip).
+// kept exactly when its fold value exceeds it (host code, fa_abi.cpp).
 uint32_t keep_threshold(float p);
 
 // dtype-specific launchers: fa_kernels_{bf16,f16,f32}.hip without a bias,

@@ -10,7 +10,14 @@ not load the library; the first kernel call does, and raises
 ``FlashAttentionExtensionError`` if it is missing.
 """
 from ._lib import FlashAttentionExtensionError, FlashAttentionKernelError  # noqa: F401
-from .interface import flash_attention_v100, validate_inputs_enhanced  # noqa: F401
+from .interface import (  # noqa: F401
+    flash_attention_memory_mode,
+    flash_attention_performance_mode,
+    flash_attention_v100,
+    flash_attention_v100_causal,
+    flash_attention_v100_with_dropout,
+    validate_inputs_enhanced,
+)
 from .kernels import (  # noqa: F401
     flash_attention_backward_triton_enhanced,
     flash_attention_forward_autotuned_enhanced,
@@ -24,11 +31,17 @@ from .ops.attention import (  # noqa: F401
     flash_attention_backward,
     flash_attention_forward,
 )
+from .modules import EnhancedMultiHeadAttention  # noqa: F401
 
 __version__ = "0.1.0"
 
 __all__ = [
     "flash_attention_v100",
+    "flash_attention_v100_causal",
+    "flash_attention_v100_with_dropout",
+    "flash_attention_performance_mode",
+    "flash_attention_memory_mode",
+    "EnhancedMultiHeadAttention",
     "FlashAttentionV100Function",
     "EnhancedFlashAttentionV100Function",
     "flash_attention_forward_triton_enhanced",

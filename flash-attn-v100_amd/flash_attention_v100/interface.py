@@ -20,6 +20,7 @@ no CPU path).
 """
 from __future__ import annotations
 
+import contextlib
 import math
 import warnings
 from typing import Optional, Tuple, Union
@@ -159,3 +160,47 @@ def flash_attention_v100(
         warnings.warn(f"Flash Attention failed ({e}), falling back to PyTorch implementation", UserWarning)
         _Stats.error_recovery_count += 1
         return _fallback_to_pytorch(q, k, v, scale, causal, dropout_p, bias, return_softmax_lse)
+
+
+# Convenience entry points and context managers of the reference
+# (interface.py:611-669).  The strategies select among numerically identical
+# kernel configurations here, so a performance mode only records the strategy.
+
+def flash_attention_v100_causal(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, **kwargs) -> torch.Tensor:
+    """Causal attention (reference ``interface.py:611-618``)."""
+    return flash_attention_v100(q, k, v, causal=True, **kwargs)
+
+
+def flash_attention_v100_with_dropout(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dropout_p: float,
+                                      **kwargs) -> torch.Tensor:
+    """Attention with dropout (reference ``interface.py:621-629``)."""
+    return flash_attention_v100(q, k, v, dropout_p=dropout_p, **kwargs)
+
+
+_current_strategy = ["balanced"]
+
+
+def current_optimization_strategy() -> str:
+    """The strategy set by the innermost :func:`flash_attention_performance_mode`."""
+    return _current_strategy[-1]
+
+
+@contextlib.contextmanager
+def flash_attention_performance_mode(strategy: str = "speed"):
+    """Run a region under an optimization strategy (reference
+    ``interface.py:644-654``, which swapped its global Manager).  The strategy is
+    validated and exposed through :func:`current_optimization_strategy`."""
+    if strategy not in _STRATEGIES:
+        raise ValueError(f"optimization_strategy must be one of {_STRATEGIES}, got {strategy!r}")
+    _current_strategy.append(strategy)
+    try:
+        yield
+    finally:
+        _current_strategy.pop()
+
+
+@contextlib.contextmanager
+def flash_attention_memory_mode():
+    """``flash_attention_performance_mode('memory')`` (reference ``interface.py:657-661``)."""
+    with flash_attention_performance_mode("memory"):
+        yield
