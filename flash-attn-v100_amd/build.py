@@ -57,6 +57,13 @@ def common_flags():
         # keep MFMA accumulators in VGPR form: without it the register allocator
         # parks the dK/dV accumulators in AGPRs and copies them every iteration
         "-mllvm", "-amdgpu-mfma-vgpr-form=true",
+        # no implicit contraction: every fused multiply-add is an explicit
+        # __builtin_fmaf in the source.  With contraction on, the compiler may
+        # fuse a product with its fp32 -> fp16 conversion (v_fma_mixlo_f16, one
+        # rounding instead of two) in some instantiations and not in others, so
+        # paths meant to be bit-identical (stored vs regenerated dropout mask)
+        # could differ by an ulp
+        "-ffp-contract=off",
         "-Wall",
         "-Wno-unused-command-line-argument",
     ]
