@@ -23,17 +23,11 @@ OBJDIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "flash_attention_v100", "libfa_gfx950.so")
 ARCH = "gfx950"
 
-SOURCES = [
-    "fa_abi.cpp",
-    "fa_misc.hip",
-    "fa_kernels_bf16.hip",
-    "fa_kernels_f16.hip",
-    "fa_kernels_f32.hip",
-    "fa_bias_bf16.hip",
-    "fa_bias_f16.hip",
-    "fa_bias_f32.hip",
-    "fa_bias32_bf16.hip",
-    "fa_bias32_f16.hip",
+SOURCES = ["fa_abi.cpp", "fa_misc.hip"] + [
+    f"fa_{pas}_{mode}{dt}.hip"
+    for pas in ("bwd", "fwd")  # the backward units take longest: start them first
+    for mode, dts in (("", ("bf16", "f16", "f32")), ("bias_", ("bf16", "f16", "f32")), ("bias32_", ("bf16", "f16")))
+    for dt in dts
 ]
 
 

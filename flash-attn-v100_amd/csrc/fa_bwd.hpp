@@ -177,13 +177,14 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value && !(Elem<T>::kF32 &&
         char* bp = buf(s);
         const T* src = copy_q ? (const T*)p.q + b * p.q_sb + (int64_t)qb0 * p.q_ss + hh * p.q_sh
                               : (const T*)p.dout + b * p.do_sb + (int64_t)qb0 * p.do_ss + hh * p.do_sh;
-        rows.load(src, copy_q ? p.q_ss : p.do_ss, p.Sq - qb0, (T*)(bp + (copy_q ? 0 : C::QALLOC)));
+        // copies the compiler does not track: it would otherwise make the
+        // next LDS read of the current tile wait for them (sync_tiles waits)
+        rows.load_untracked(src, copy_q ? p.q_ss : p.do_ss, p.Sq - qb0, (const T*)(bp + (copy_q ? 0 : C::QALLOC)));
         const float* wrow = p.lse2 + ((int64_t)b * p.H + hh) * p.ws_stride + qb0;  // qb0 + BQ <= sq_pad
-        const __amdgpu_buffer_rsrc_t rs =
-            __builtin_amdgcn_make_buffer_rsrc((void*)wrow, (short)0, (p.ws_stride - qb0) * 4, 0x00020000);
-        float* f = (float*)(bp + 2 * C::QALLOC);
-        dma_load4(rs, f, 4 * lane);                 // LSE * log2 e
-        dma_load4(rs, f + BQ, 4 * (p.sq_pad + lane));  // delta
+        const u32x4 rs = buffer_words(wrow, (p.ws_stride - qb0) * 4);
+        const uint32_t f = lds_addr(bp + 2 * C::QALLOC);
+        dma_load4_untracked(rs, f, 4 * lane);                       // LSE * log2 e
+        dma_load4_untracked(rs, f + 4 * BQ, 4 * (p.sq_pad + lane));  // delta
     };
     // direct-to-LDS copies complete when the issuing wave's vmcnt drains
     auto sync_tiles = [&]() {
@@ -561,7 +562,9 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
     auto issue = [&](int j, int s) FA_INLINE {
         const int k0 = j * BN;
         const T* src = copy_k ? kbase + (int64_t)k0 * p.k_ss : vbase + (int64_t)k0 * p.v_ss;
-        rows.load(src, copy_k ? p.k_ss : p.v_ss, p.Sk - k0, (T*)(buf(s) + (copy_k ? 0 : C::KALLOC)));
+        // copies the compiler does not track: it would otherwise make the
+        // next LDS read of the current tile wait for them (sync_tiles waits)
+        rows.load_untracked(src, copy_k ? p.k_ss : p.v_ss, p.Sk - k0, (const T*)(buf(s) + (copy_k ? 0 : C::KALLOC)));
     };
     // direct-to-LDS copies complete when the issuing wave's vmcnt drains
     auto sync_tiles = [&]() {

@@ -1,0 +1,12 @@
+// Backward kernel instantiations (delta pre-pass, dK/dV, dQ) for bf16 inputs (D in
+// {32, 64, 128}, causal x dropout), with an additive bias of the input dtype.  One translation unit per pass,
+// dtype and bias mode keeps builds parallel.
+#include "fa_bwd.hpp"
+
+namespace fa {
+
+hipError_t launch_bwd_bias_bf16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s) {
+    return launch_bwd_dispatch<bf16, bf16>(p, D, causal, dropout, stage, s);
+}
+
+}  // namespace fa

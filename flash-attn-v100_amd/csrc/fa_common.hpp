@@ -232,6 +232,17 @@ __device__ FA_INLINE inline void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Workgroup barrier without a memory fence, for loops that order their LDS
+// traffic explicitly: a release fence would make the compiler wait for every
+// direct-to-LDS copy still in flight (vmcnt(0)), including copies issued just
+// before the barrier for a later tile.  The empty asm statements keep the
+// compiler from moving memory accesses across the barrier.
+__device__ FA_INLINE inline void barrier_no_fence() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // ---------------------------------------------------------------------------
 // LDS access
 typedef __attribute__((address_space(3))) void lds_void;
@@ -332,6 +343,14 @@ __device__ FA_INLINE inline __amdgpu_buffer_rsrc_t row_buffer(const T* base, int
 // not re-wait for them (together with the next tile's prefetch) each iteration.
 __device__ FA_INLINE inline void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
+// Wait until at most N vector-memory operations of this wave are outstanding
+// (they complete in issue order); expcnt and lgkmcnt are not waited for.
+template <int N>
+__device__ FA_INLINE inline void wait_vmem_below() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
 // ---------------------------------------------------------------------------
 // One 16-byte-per-lane global -> LDS load (buffer_load_dwordx4 ... lds): lane
 // l writes LDS bytes [16 l, 16 l + 16) past `lds`, which must be wave-uniform.
@@ -341,6 +360,53 @@ __device__ FA_INLINE inline void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70
 template <typename T>
 __device__ FA_INLINE inline void dma_load16(__amdgpu_buffer_rsrc_t rs, T* lds, int byte_offset) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, byte_offset, 0, 0, 0);
+}
+
+// The same 16-byte-per-lane copy issued from inline assembly, for loops that
+// order their copies themselves with explicit vmcnt waits.  The compiler does
+// not see it as an LDS write, so it does not make the next LDS read of any
+// slot wait for every copy in flight (it cannot tell the slots apart), and it
+// does not count it in its own vmcnt waits: those can only wait longer than
+// needed (vector-memory operations complete in issue order), never shorter.
+// The caller waits for the copy (s_waitcnt vmcnt) before any wave reads its
+// destination.  `rs` is the buffer descriptor as four wave-uniform dwords,
+// `lds` the LDS byte address of lane 0's chunk (wave-uniform).
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+__device__ FA_INLINE inline void dma_load16_untracked(const u32x4& rs, uint32_t lds, int byte_offset) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %1, %2, 0 offen lds"
+        :
+        : "s"(lds), "v"(byte_offset), "s"(rs)
+        : "memory", "m0");
+}
+
+// Four-dword descriptor of `bytes` bytes at `base` (wave-uniform), for the
+// untracked copies
+__device__ FA_INLINE inline u32x4 buffer_words(const void* base, int bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    u32x4 w;
+    w[0] = __builtin_amdgcn_readfirstlane((unsigned)a);
+    w[1] = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32) & 0xFFFFu);
+    w[2] = __builtin_amdgcn_readfirstlane((unsigned)bytes);
+    w[3] = 0x00020000u;
+    return w;
+}
+
+// Four-dword buffer descriptor of the rows [0, min(nvalid, R)) of a tile, as
+// row_buffer builds it (raw untyped dword access, no stride, no swizzle).
+template <typename T, int D, int R>
+__device__ FA_INLINE inline u32x4 row_buffer_words(const T* base, int64_t row_stride, int nvalid) {
+    const int nv = min(max(nvalid, 0), R);
+    const int bytes = ((nv - 1) * (int)row_stride + D) * (int)sizeof(T) * min(nv, 1);
+    return buffer_words(base, bytes);
+}
+
+// LDS byte address of a __shared__ object (an address-space cast, then the
+// 32-bit LDS offset)
+__device__ FA_INLINE inline uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
 // ---------------------------------------------------------------------------
@@ -390,6 +456,73 @@ struct DmaTile {
             }
         }
     }
+    // the same copy, not tracked by the compiler (see dma_load16_untracked):
+    // the caller waits for it (vmcnt) before the barrier that publishes it
+    __device__ FA_INLINE inline void load_untracked(const T* base, int64_t row_stride, int nvalid, const T* lds,
+                                                    int lane) const {
+        static_assert(CHUNKS % 64 == 0, "whole instructions (an idle lane would need its own exec mask)");
+        const u32x4 rs = row_buffer_words<T, D, R>(base, row_stride, nvalid);
+        const uint32_t l0 = lds_addr(lds);
+#pragma unroll
+        for (int t = 0; t < PER; ++t) {
+            const int g = wave + NW * t;
+            if (NI % NW == 0 || g < NI) dma_load16_untracked(rs, l0 + 64 * 16 * g, off[t]);
+        }
+    }
+};
+
+// Direct global -> LDS copy of a K tile and a V tile ([R][D] each, LDS row
+// strides KW and VW), as one list of copy instructions (the K tile's, then the
+// V tile's) dealt round-robin to NW waves, so that every wave issues the same
+// number of them when NW divides the total (a partial vmcnt wait can then
+// leave exactly the newest pair of tiles in flight).  Layout of each tile as in
+// DmaTile (64 consecutive 16-byte LDS chunks per instruction, padding chunks
+// read nothing, rows >= nvalid land as zeros).
+template <typename T, int R, int D, int KW, int VW, int NW>
+struct DmaTilePair {
+    static constexpr int EPC = 16 / (int)sizeof(T);
+    static constexpr int CD = D / EPC;
+    static constexpr int CWK = KW / EPC, CWV = VW / EPC;
+    static_assert(D % EPC == 0 && KW % EPC == 0 && VW % EPC == 0 && KW >= D && VW >= D, "16-byte chunked rows");
+    static_assert((R * CWK) % 64 == 0 && (R * CWV) % 64 == 0, "whole instructions per tile");
+    static constexpr int NK = R * CWK / 64;
+    static constexpr int NV = R * CWV / 64;
+    static constexpr int NI = NK + NV;
+    static constexpr int PER = (NI + NW - 1) / NW;
+    static constexpr int MIN_PER = NI / NW;  // instructions issued by every wave
+    int off[PER];
+    int wave;
+
+    __device__ FA_INLINE inline void init(int64_t k_stride, int64_t v_stride, int lane, int wave_id) {
+        wave = wave_id;
+#pragma unroll
+        for (int t = 0; t < PER; ++t) {
+            const int g = wave + NW * t;
+            const bool is_k = g < NK;
+            const int cw = is_k ? CWK : CWV;
+            const int c = 64 * (is_k ? g : g - NK) + lane;
+            const int row = c / cw, col = c % cw;
+            const int64_t st = is_k ? k_stride : v_stride;
+            off[t] = col < CD ? (row * (int)st + col * EPC) * (int)sizeof(T) : kOffNowhere;
+        }
+    }
+    // Both tiles, with copies the compiler does not track (see
+    // dma_load16_untracked): the caller orders them with explicit vmcnt waits.
+    // A tile past the sequence (nvalid <= 0) reads nothing and lands as zeros.
+    __device__ FA_INLINE inline void load_untracked(const T* kb, int64_t k_stride, int k_valid, const T* k_lds,
+                                                    const T* vb, int64_t v_stride, int v_valid, const T* v_lds) const {
+        const u32x4 rk = row_buffer_words<T, D, R>(kb, k_stride, k_valid);
+        const u32x4 rv = row_buffer_words<T, D, R>(vb, v_stride, v_valid);
+        const uint32_t lk = lds_addr(k_lds), lv = lds_addr(v_lds);
+#pragma unroll
+        for (int t = 0; t < PER; ++t) {
+            const int g = wave + NW * t;
+            if (g < NK)
+                dma_load16_untracked(rk, lk + 64 * 16 * g, off[t]);
+            else if (NI % NW == 0 || g < NI)
+                dma_load16_untracked(rv, lv + 64 * 16 * (g - NK), off[t]);
+        }
+    }
 };
 
 // Direct global -> LDS copy of a [R][D] tile where each wave instruction
@@ -431,7 +564,35 @@ struct DmaRowGroups {
                 dma_load16(rs, lds + g * KR * W, off + g * KR * (int)row_stride * (int)sizeof(T));
         }
     }
+    // the same copy, not tracked by the compiler (see dma_load16_untracked):
+    // the caller waits for it (vmcnt) before the barrier that publishes it.
+    // Idle lanes (past the group's rows) are switched off by the branch, which
+    // masks exec around the assembly.
+    __device__ FA_INLINE inline void load_untracked(const T* base, int64_t row_stride, int nvalid, const T* lds) const {
+        const u32x4 rs = row_buffer_words<T, D, R>(base, row_stride, nvalid);
+        const uint32_t l0 = lds_addr(lds);
+#pragma unroll
+        for (int t = 0; t < PER; ++t) {
+            const int g = wave + NWAVES * t;
+            const int rows_here = (R % KR == 0 || g < NI - 1) ? KR : R - (NI - 1) * KR;
+            if ((NI % NWAVES == 0 || g < NI) && rowl < rows_here)
+                dma_load16_untracked(rs, l0 + g * KR * W * (int)sizeof(T), off + g * KR * (int)row_stride * (int)sizeof(T));
+        }
+    }
 };
+
+// One dword per lane global -> LDS, not tracked by the compiler (see
+// dma_load16_untracked): lane l writes LDS bytes [4 l, 4 l + 4) past the LDS
+// byte address `lds` (wave-uniform).
+__device__ FA_INLINE inline void dma_load4_untracked(const u32x4& rs, uint32_t lds, int byte_offset) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %2, 0 offen lds"
+        :
+        : "s"(lds), "v"(byte_offset), "s"(rs)
+        : "memory", "m0");
+}
 
 // One dword per lane global -> LDS (buffer_load_dword ... lds): lane l writes
 // LDS bytes [4 l, 4 l + 4) past `lds` (wave-uniform).

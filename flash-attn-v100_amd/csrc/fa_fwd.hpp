@@ -163,13 +163,21 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     const int wv = __builtin_amdgcn_readfirstlane(w);
     DmaTile<T, BN, D, KW, C::NW> kdma;
     kdma.init(p.k_ss, lane, wv);
+    // 16-bit tiles: copies the compiler does not track, which it would
+    // otherwise make the next LDS read wait for (sync_tiles waits for them)
     auto dma_k = [&](int j, int slot) {
-        kdma.load(kbase + (int64_t)(j * BN) * p.k_ss, p.k_ss, p.Sk - j * BN, Ks0 + slot * C::KTILE, lane);
+        if constexpr (C::F32)
+            kdma.load(kbase + (int64_t)(j * BN) * p.k_ss, p.k_ss, p.Sk - j * BN, Ks0 + slot * C::KTILE, lane);
+        else
+            kdma.load_untracked(kbase + (int64_t)(j * BN) * p.k_ss, p.k_ss, p.Sk - j * BN, Ks0 + slot * C::KTILE, lane);
     };
     DmaTile<T, BN, D, VW, C::NW> vst;
     vst.init(p.v_ss, lane, wv);
     auto load_v = [&](int j, int slot) {
-        vst.load(vbase + (int64_t)(j * BN) * p.v_ss, p.v_ss, p.Sk - j * BN, Vs0 + slot * C::VTILE, lane);
+        if constexpr (C::F32)
+            vst.load(vbase + (int64_t)(j * BN) * p.v_ss, p.v_ss, p.Sk - j * BN, Vs0 + slot * C::VTILE, lane);
+        else
+            vst.load_untracked(vbase + (int64_t)(j * BN) * p.v_ss, p.v_ss, p.Sk - j * BN, Vs0 + slot * C::VTILE, lane);
     };
 
     // ---- S^T = K Q^T for one key tile ----
@@ -421,8 +429,344 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Ping-pong forward for 16-bit inputs without bias or dropout (the large-grid
+// case).  One workgroup = 8 waves = 256 queries of one (batch, head); waves w
+// and w + 4 run on the same SIMD (the hardware deals the waves of a workgroup
+// to SIMDs 0, 2, 1, 3, 0, 2, 1, 3).  Every wave runs the same program,
+//   for each key tile r:  M(r) | barrier | V(r) | barrier
+//   M(r): S(r) = K(r) Q^T (if the wave needs key tile r), O^T += V(r-1)^T P(r-1)
+//   V(r): mask (diagonal / tail tiles), running max, P(r) = exp2(...) packed
+// but waves 4-7 pass one extra barrier first (and waves 0-3 one at the end),
+// so the two waves of a SIMD run one phase apart: while one issues its matrix
+// products, the other runs its softmax.  Every barrier is workgroup-wide.
+// K and V tiles (global -> LDS, read by all 8 waves) rotate through four
+// slots.  Waves 0-3 copy them: in the V phase of tile r each issues its share
+// of K(r+3) and V(r+2) (the same number of copy instructions per wave), after
+// waiting for its copies of two V phases ago, which the barrier closing the
+// phase then publishes; a copy thus has two rounds to land, and a slot is only
+// overwritten after both groups have read its previous tile.  Per query the arithmetic is that of fwd_kernel (same tile order,
+// same lazy rescale per 32-query wave), so the outputs are bit-identical to it.
+template <typename T, int D>
+struct FwdPPCfg {
+    static constexpr int NW = 8;
+    static constexpr int NT = 64 * NW;
+    static constexpr int BM = 32 * NW;            // queries per workgroup
+    static constexpr int BN = 64;                 // keys per tile
+    static constexpr int NB = BN / 32;            // 32-key blocks per tile
+    static constexpr int NSLOT = 4;               // K / V tile slots
+    static constexpr int KW = D + 8;              // K row stride (elements)
+    static constexpr int VW = D + (D == 64 ? 8 : 24);
+    static constexpr int KTILE = BN * KW;
+    static constexpr int VTILE = BN * VW;
+    static constexpr int OW = D + 8;              // output staging row stride
+    static constexpr int SMEM_ELEMS = NSLOT * (KTILE + VTILE);
+    static_assert(NW * 32 * OW <= SMEM_ELEMS, "O staging must fit in the K/V buffers");
+    static_assert(SMEM_ELEMS * 2 <= 160 * 1024, "LDS of one CU");
+};
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const FwdParams p) {
+    using C = FwdPPCfg<T, D>;
+    static_assert(!Elem<T>::kF32, "16-bit inputs");
+    constexpr int BN = C::BN, NB = C::NB, KW = C::KW, VW = C::VW, NSLOT = C::NSLOT;
+    __shared__ __attribute__((aligned(16))) T smem[C::SMEM_ELEMS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
+    const int grp = w >> 2;
+    // the two waves of a SIMD own adjacent 32-query blocks (similar causal work)
+    const int blk = 2 * (w & 3) + grp;
+
+    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = L / p.n_qtiles;
+    const int qt = p.n_qtiles - 1 - (L - bh * p.n_qtiles);  // longest causal rows first
+    const int h = bh % p.H, b = bh / p.H;
+    const int hk = h / p.group;
+    const int q0 = qt * C::BM;
+    const int qw0 = q0 + 32 * blk;
+    const int qi = qw0 + l32;
+
+    const T* __restrict__ kbase = (const T*)p.k + b * p.k_sb + hk * p.k_sh;
+    const T* __restrict__ vbase = (const T*)p.v + b * p.v_sb + hk * p.v_sh;
+
+    int kv_end = p.Sk;
+    if (CAUSAL) kv_end = min(kv_end, min(q0 + C::BM, p.Sq));
+    const int n_tiles = (kv_end + BN - 1) / BN;
+    // key tiles this wave uses, and how many of them need no mask
+    int n_w = qw0 < p.Sq ? n_tiles : 0;
+    if (CAUSAL) n_w = min(n_w, (qw0 + 31) / BN + 1);
+    int n_um = min(n_w, p.Sk / BN);
+    if (CAUSAL) n_um = min(n_um, (qw0 + 1) / BN);
+
+    // ---- Q into registers (MFMA B operand): d = 16 i + 8 hi .. +7 ----
+    constexpr int QR = D / 16;
+    uint4 qreg[QR];
+    {
+        const T* qrow = (const T*)p.q + b * p.q_sb + (int64_t)qi * p.q_ss + h * p.q_sh;
+#pragma unroll
+        for (int i = 0; i < QR; ++i)
+            qreg[i] = qi < p.Sq ? *reinterpret_cast<const uint4*>(qrow + 16 * i + 8 * hi) : make_uint4(0u, 0u, 0u, 0u);
+    }
+
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) o[i] = f32x16{};
+    float m_run = -1e30f;  // running max in log2 units
+    float l_run = 0.f;     // lane-partial row sum
+    float m_raw = -INFINITY;
+    const float c = p.scale_log2;
+
+    T* Ks0 = smem;
+    T* Vs0 = smem + NSLOT * C::KTILE;
+    // prologue copies: all 8 waves; in the loop: waves 0-3, K(j) with V(j-1)
+    DmaTile<T, BN, D, KW, C::NW> kdma;
+    kdma.init(p.k_ss, lane, w);
+    DmaTile<T, BN, D, VW, C::NW> vdma;
+    vdma.init(p.v_ss, lane, w);
+    auto dma_k = [&](int j) FA_INLINE {
+        if (j < n_tiles)
+            kdma.load(kbase + (int64_t)(j * BN) * p.k_ss, p.k_ss, p.Sk - j * BN, Ks0 + (j % NSLOT) * C::KTILE, lane);
+    };
+    auto dma_v = [&](int j) FA_INLINE {
+        if (j < n_tiles)
+            vdma.load(vbase + (int64_t)(j * BN) * p.v_ss, p.v_ss, p.Sk - j * BN, Vs0 + (j % NSLOT) * C::VTILE, lane);
+    };
+    using Pair = DmaTilePair<T, BN, D, KW, VW, 4>;
+    Pair kvdma;
+    kvdma.init(p.k_ss, p.v_ss, lane, w & 3);
+    // K(j) and V(j - 1).  Issued whole even past the last tile (a tile past
+    // Sk has an empty buffer range: nothing is read and its slot, whose tile
+    // both groups have finished, fills with zeros), so that every batch of a
+    // wave has at least Pair::MIN_PER copy instructions.
+    auto dma_kv = [&](int j) FA_INLINE {
+        kvdma.load_untracked(kbase + (int64_t)(j * BN) * p.k_ss, p.k_ss, p.Sk - j * BN, Ks0 + (j % NSLOT) * C::KTILE,
+                             vbase + (int64_t)((j - 1) * BN) * p.v_ss, p.v_ss, p.Sk - (j - 1) * BN,
+                             Vs0 + ((j - 1) % NSLOT) * C::VTILE);
+    };
+
+    f32x16 s[NB];        // scores of tile r between its M and V phases
+    s16x8 pk[BN / 16];   // P of tile r between its V phase and the M phase of tile r+1
+
+    // ---- M phase of tile r: S(r) = K(r) Q^T, O^T += V(r-1)^T P(r-1) ----
+    // Step t issues the t-th S product and the t-th PV product; the LDS
+    // operands of step t + MP are read during step t (MP steps ahead), so no
+    // product waits out an LDS latency.
+    const int trow = 4 * hi + ((lane & 15) >> 2);
+    const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    constexpr int NQK = NB * QR;               // S MFMAs per tile
+    constexpr int NPV = (BN / 16) * (D / 32);  // PV MFMAs per tile
+    static_assert(NQK == NPV, "one S and one PV product per step");
+    constexpr int NSTEP = NQK;
+    constexpr int MP = 3;
+    auto kfrag = [&](const T* Ks, int t) FA_INLINE {
+        const int bk = t / QR, kk = t % QR;
+        return *reinterpret_cast<const s16x8*>(Ks + (32 * bk + l32) * KW + 16 * kk + 8 * hi);
+    };
+    auto vfrag = [&](const T* Vs, int t) FA_INLINE {
+        const int ks = t / (D / 32), i = t % (D / 32);
+        const T* vp = Vs + (16 * ks + trow) * VW + 32 * i + tcol;
+        return cat4(lds_read_tr16(vp), lds_read_tr16(vp + 8 * VW));
+    };
+    auto qk_mfma = [&](const s16x8& a, int t) FA_INLINE {
+        const int bk = t / QR, kk = t % QR;
+        s[bk] = Elem<T>::mfma(a, __builtin_bit_cast(s16x8, qreg[kk]), kk == 0 ? f32x16{} : s[bk]);
+    };
+    auto pv_mfma = [&](const s16x8& a, int t) FA_INLINE {
+        const int ks = t / (D / 32), i = t % (D / 32);
+        o[i] = Elem<T>::mfma(a, pk[ks], o[i]);
+    };
+    // QK: S(r) only (the first tile); PV: O += V(r-1) P(r-1) only (the tile after a wave's last)
+    auto mphase = [&](int r, auto qk_tag, auto pv_tag) FA_INLINE {
+        constexpr bool QK = decltype(qk_tag)::value, PV = decltype(pv_tag)::value;
+        const T* Ks = Ks0 + (r % NSLOT) * C::KTILE;
+        const T* Vs = Vs0 + ((r + NSLOT - 1) % NSLOT) * C::VTILE;
+        s16x8 kf[NSTEP], vf[NSTEP];
+#pragma unroll
+        for (int t = 0; t < MP; ++t) {
+            if (QK) kf[t] = kfrag(Ks, t);
+            if (PV) vf[t] = vfrag(Vs, t);
+        }
+#pragma unroll
+        for (int t = 0; t < NSTEP; ++t) {
+            if (t + MP < NSTEP) {
+                if (QK) kf[t + MP] = kfrag(Ks, t + MP);
+                if (PV) vf[t + MP] = vfrag(Vs, t + MP);
+            }
+            if (QK) qk_mfma(kf[t], t);
+            if (PV) pv_mfma(vf[t], t);
+        }
+        // the same order for the scheduler: reads of MP steps, then per step
+        // its products followed by the reads of step t + MP
+        constexpr int RD = (QK ? 1 : 0) + (PV ? 2 : 0);
+        constexpr int MF = (QK ? 1 : 0) + (PV ? 1 : 0);
+#pragma unroll
+        for (int t = 0; t < MP; ++t) __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
+#pragma unroll
+        for (int t = 0; t < NSTEP; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
+            if (t + MP < NSTEP) __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);
+        }
+    };
+
+    // ---- V phase of tile r: mask, running max (lazy rescale), P(r) ----
+    auto vphase = [&](int r) FA_INLINE {
+        if (r >= n_um) {
+            const int k0 = r * BN;
+#pragma unroll
+            for (int bk = 0; bk < NB; ++bk)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int key = k0 + 32 * bk + 8 * (e >> 2) + 4 * hi + (e & 3);
+                    if (key >= p.Sk || (CAUSAL && key > qi)) s[bk][e] = -INFINITY;
+                }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int bk = 0; bk < NB; ++bk)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[bk][e]);
+        mx = pair_max(mx);
+        m_raw = fmaxf(m_raw, mx);
+        const float m_new = fmaxf(m_run, mx * c);
+        if (__ballot(m_new > m_run + 8.0f) != 0ull) {
+            const float alpha = fast_exp2(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+            m_run = m_new;
+        }
+        float psum = 0.f;
+#pragma unroll
+        for (int bk = 0; bk < NB; ++bk)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float pv = fast_exp2(__builtin_fmaf(s[bk][e], c, -m_run));
+                psum += pv;
+                s[bk][e] = pv;
+            }
+        l_run += psum;
+#pragma unroll
+        for (int ks = 0; ks < BN / 16; ++ks) {
+            float tmp[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) tmp[e] = s[ks >> 1][8 * (ks & 1) + e];
+            pk[ks] = pack8<T>(tmp);
+        }
+    };
+
+    auto sched_fence = [&]() FA_INLINE { __builtin_amdgcn_sched_barrier(0); };
+    // one round: M phase, barrier, V phase (wait for the previous copies,
+    // issue the next ones), barrier
+    auto round = [&](int r, auto qk_tag, auto pv_tag, auto v_tag) FA_INLINE {
+        sched_fence();
+        if constexpr (decltype(qk_tag)::value || decltype(pv_tag)::value) mphase(r, qk_tag, pv_tag);
+        sched_fence();
+        barrier_no_fence();
+        sched_fence();
+        if constexpr (decltype(v_tag)::value) vphase(r);
+        if (grp == 0) {
+            // this wave's copies of two V phases ago have landed (at most the
+            // last batch, >= MIN_PER instructions, is still in flight): the
+            // barrier below publishes them.  Then K(r+3) replaces K(r-1) and
+            // V(r+2) replaces V(r-2), both last read in M(r-1), which both
+            // groups have finished.
+            wait_vmem_below<Pair::MIN_PER>();
+            dma_kv(r + 3);
+        }
+        sched_fence();
+        // no release fence: it would wait for the copies just issued.  The
+        // wait above orders this wave's landed copies before the barrier, and
+        // every LDS read of M(r) has completed (its products consumed it).
+        barrier_no_fence();
+    };
+    using TT = std::true_type;
+    using FF = std::false_type;
+
+    // prologue: the tiles the first three M phases read
+    dma_k(0);
+    dma_k(1);
+    dma_k(2);
+    dma_v(0);
+    dma_v(1);
+    wait_vmem();
+    lds_barrier();
+    if (grp == 1) barrier_no_fence();  // waves 4-7 run one phase behind
+    // rounds 0 .. n_tiles: S(0) alone; S(r) with P(r-1) V(r-1) while the wave
+    // needs tile r; P V of its last tile; then only the copies
+    int r = 0;
+    if (n_w > 0) {
+        round(0, TT{}, FF{}, TT{});
+        for (r = 1; r < n_w; ++r) round(r, TT{}, TT{}, TT{});
+        round(r, FF{}, TT{}, FF{});
+        ++r;
+    }
+    for (; r <= n_tiles; ++r) round(r, FF{}, FF{}, FF{});
+    if (grp == 0) barrier_no_fence();
+    sched_fence();
+
+    // ---- epilogue: normalise, LSE, stage O^T through LDS, coalesced store ----
+    const float l_tot = pair_sum(l_run);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    if (hi == 0 && qi < p.Sq) {
+        const int64_t si = (int64_t)(b * p.H + h) * p.Sq + qi;
+        p.lse[si] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
+        if (p.mx) p.mx[si] = m_raw * p.scale;
+    }
+    wait_vmem();     // no copy in flight (the last ones target unused slots)
+    lds_barrier();   // every wave is done with the K / V slots
+    constexpr int OW = C::OW;
+    T* Os = smem + w * 32 * OW;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d = 32 * i + 8 * g + 4 * hi;
+            s16x4 v4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v4[e] = Elem<T>::pack1(o[i][4 * g + e] * inv);
+            *reinterpret_cast<s16x4*>(Os + l32 * OW + d) = v4;
+        }
+    lds_barrier();
+    constexpr int EPC = 16 / sizeof(T);
+    constexpr int CPR = D / EPC;
+    T* obase = (T*)p.o + b * p.o_sb + h * p.o_sh;
+#pragma unroll
+    for (int i = 0; i < 32 * CPR / 64; ++i) {
+        const int cidx = lane + 64 * i;
+        const int row = cidx / CPR, col = cidx % CPR;
+        const int q = qw0 + row;
+        if (q < p.Sq)
+            *reinterpret_cast<uint4*>(obase + (int64_t)q * p.o_ss + col * EPC) =
+                *reinterpret_cast<const uint4*>(Os + row * OW + col * EPC);
+    }
+}
+
+// When the ping-pong kernel runs (measured on C3/C4 shapes, D = 128): its
+// 256-query workgroups must fill the chip at least once, and with causal
+// masking only long sequences gain (it runs one workgroup per CU, so the
+// causal diagonal, where the waves of the lower query blocks have no work,
+// and each workgroup's first tile copies are not hidden by a second
+// workgroup; at S = 4096 that costs more than the shared K/V tiles save).
+inline bool fwd_pp_wanted(const FwdParams& p, bool causal) {
+    const int64_t n = (int64_t)((p.Sq + 255) / 256) * p.H * p.B;
+    return n >= 256 && (!causal || p.Sq >= 16384);
+}
+
 template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
 hipError_t launch_fwd_t(const FwdParams& p, hipStream_t s) {
+    if constexpr (!Elem<T>::kF32 && DROPOUT == 0 && std::is_void<TB>::value && D == 128) {
+        if (fwd_pp_wanted(p, CAUSAL)) {
+            using CP = FwdPPCfg<T, D>;
+            FwdParams q = p;
+            q.n_qtiles = (p.Sq + CP::BM - 1) / CP::BM;
+            const int64_t nblocks = (int64_t)q.n_qtiles * p.H * p.B;
+            hipLaunchKernelGGL((fwd_pp_kernel<T, D, CAUSAL>), dim3((unsigned)nblocks), dim3(CP::NT), 0, s, q);
+            return hipGetLastError();
+        }
+    }
     using C = FwdCfg<T, D>;
     FwdParams q = p;
     q.n_qtiles = (p.Sq + C::BM - 1) / C::BM;

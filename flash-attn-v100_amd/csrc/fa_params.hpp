@@ -102,9 +102,9 @@ constexpr int kSqPad = 128;
 // kept exactly when its fold value exceeds it (host code, fa_abi.cpp).
 uint32_t keep_threshold(float p);
 
-// dtype-specific launchers: fa_kernels_{bf16,f16,f32}.hip without a bias,
-// fa_bias_{bf16,f16,f32}.hip with a bias of the input dtype,
-// fa_bias32_{bf16,f16}.hip with a float32 bias
+// dtype-specific launchers, one translation unit per pass (fwd / bwd):
+// fa_{fwd,bwd}_{bf16,f16,f32}.hip without a bias, fa_{fwd,bwd}_bias_{bf16,f16,f32}.hip
+// with a bias of the input dtype, fa_{fwd,bwd}_bias32_{bf16,f16}.hip with a float32 bias
 hipError_t launch_fwd_bf16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
 hipError_t launch_fwd_f16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
 hipError_t launch_fwd_f32(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);

@@ -1,0 +1,75 @@
+"""Parity of the 8-wave ping-pong forward (fwd_pp_kernel), called through the C
+ABI, against the float64 oracle.
+
+The library runs that kernel for 16-bit inputs with D = 128, no bias and no
+dropout, when the 256-query workgroups fill the chip at least once
+(ceil(Sq / 256) * H * B >= 256) and the attention is non-causal or causal with
+Sq >= 16384; every shape below is chosen to meet that rule, with the edge cases
+of the tile loop (Sq and Sk not multiples of the 256-query / 64-key tiles, GQA,
+Sq != Sk, strided views, the row max).  Tolerance as for the other kernels:
+within 2x the error of the reference math run in the inputs' dtype.
+"""
+import pytest
+import torch
+
+from flash_attention_v100 import _lib
+from helpers import assert_parity, compare, make_inputs
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def routes_to_pingpong(B, Sq, H, D, causal, dtype):
+    return (dtype != torch.float32 and D == 128 and ((Sq + 255) // 256) * H * B >= 256
+            and (not causal or Sq >= 16384))
+
+
+CASES = [
+    # dtype, B, Sq, Sk, H, Hkv, causal
+    (torch.bfloat16, 2, 1000, 777, 64, 16, False),    # ragged Sq and Sk, GQA 4:1
+    (torch.float16, 4, 512, 512, 32, 32, False),      # whole tiles
+    (torch.bfloat16, 1, 300, 4101, 256, 32, False),   # Sq < Sk, GQA 8:1, one query tile
+    (torch.float16, 1, 16461, 16461, 4, 1, True),     # causal, ragged last tile, MQA
+    (torch.bfloat16, 1, 16500, 12000, 4, 2, True),    # causal with Sq > Sk (top-left)
+]
+
+
+def _id(c):
+    dt, B, Sq, Sk, H, Hkv, causal = c
+    return f"{str(dt)[6:]}-B{B}-Sq{Sq}-Sk{Sk}-H{H}-Hkv{Hkv}-{'causal' if causal else 'full'}"
+
+
+@pytest.mark.parametrize("case", CASES, ids=[_id(c) for c in CASES])
+def test_pingpong_forward(case):
+    dt, B, Sq, Sk, H, Hkv, causal = case
+    assert routes_to_pingpong(B, Sq, H, 128, causal, dt)
+    say(f"case: ping-pong forward {_id(case)}")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, Sq, H, 128, dt, Sk=Sk, Hkv=Hkv, seed=21))
+    scale = 128 ** -0.5
+    o, lse, mx = _lib.fwd(q, k, v, causal, scale, want_max=True)
+    torch.cuda.synchronize()
+    res = compare(q, k, v, do, causal, scale, (o, lse), with_bwd=False, hpc=4)
+    assert_parity(res, dt, _id(case))
+    # row max of the scaled scores (max_vals), one batch / head checked in float64
+    s = torch.matmul(q[0, :, 0].double(), k[0, :, 0].double().t().contiguous()) * scale
+    if causal:
+        s = s.masked_fill(torch.ones_like(s, dtype=torch.bool).triu(1), float("-inf"))
+    assert torch.allclose(mx[0, 0].double(), s.amax(-1), atol=1e-4, rtol=1e-5)
+
+
+def test_pingpong_strided_and_deterministic():
+    B, S, H, D = 2, 1024, 64, 128
+    say(f"case: ping-pong forward (B,H,S,D)-major views and two runs, ({B},{S},{H},{D}) bf16")
+    assert routes_to_pingpong(B, S, H, D, False, torch.bfloat16)
+    q, k, v, _ = (t.to(DEV) for t in make_inputs(B, S, H, D, torch.bfloat16, seed=22))
+    qs, ks, vs = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v))
+    a = _lib.fwd(q, k, v, False, D ** -0.5)[:2]
+    b = _lib.fwd(qs, ks, vs, False, D ** -0.5)[:2]
+    c = _lib.fwd(q, k, v, False, D ** -0.5)[:2]
+    torch.cuda.synchronize()
+    for x, y, z in zip(a, b, c):
+        assert torch.equal(x, y) and torch.equal(x, z)
