@@ -45,7 +45,13 @@ CASES = [  # dtype, B, Sq, Sk, H, Hkv, D, causal
     (torch.float32, 1, 70, 70, 2, 1, 128, True),
     (torch.bfloat16, 1, 1, 50, 2, 1, 64, False),      # one query
     (torch.float16, 1, 64, 1, 2, 2, 128, False),      # one key
-    (torch.float16, 8, 1000, 1000, 16, 16, 128, True),  # C5 shape
+    # the benchmark's C5 edge sweep at full size, every head dim and dtype
+    (torch.float16, 8, 1000, 1000, 16, 16, 32, True),
+    (torch.float16, 8, 1000, 1000, 16, 16, 64, True),
+    (torch.float16, 8, 1000, 1000, 16, 16, 128, True),
+    (torch.float32, 8, 1000, 1000, 16, 16, 32, True),
+    (torch.float32, 8, 1000, 1000, 16, 16, 64, True),
+    (torch.float32, 8, 1000, 1000, 16, 16, 128, True),
     (torch.bfloat16, 2, 77, 90, 3, 3, 64, True),      # odd Sq: row pairs of the mask kernel span two heads
     (torch.float16, 1, 33, 600, 2, 1, 128, True),     # odd Sq, keys past the longest causal row
 ]
