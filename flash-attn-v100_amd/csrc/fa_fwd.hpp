@@ -52,18 +52,26 @@ struct FwdCfg {
     static_assert(NW * 32 * OW <= SMEM_ELEMS, "O staging must fit in the K/V buffers");
 };
 
-// TB: element type of the additive bias (T or float), void = no bias
-template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
-__global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
+// TB: element type of the additive bias (T or float), void = no bias.
+// KS: key split.  With KS > 1 the workgroup has KS groups of 4 waves on the
+// same 128 queries; group sp walks key tiles sp, sp + KS, ... through its own
+// double-buffered LDS tiles, and the partial (max, sum, O) of the groups are
+// merged through LDS at the end (exactly: each part is rescaled to the common
+// maximum).  Small grids use it: a workgroup's key loop is a serial chain of
+// tile latencies, and KS groups walk it KS times shorter on the same CU.
+template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB, int KS>
+__global__ __launch_bounds__(256 * KS, KS == 1 ? 2 : 1) void fwd_kernel(const FwdParams p) {
     using C = FwdCfg<T, D>;
     constexpr bool BIAS = !std::is_void<TB>::value;
     using BT = typename std::conditional<BIAS, TB, T>::type;
     constexpr int BN = C::BN, NB = C::NB, KW = C::KW, VW = C::VW;
-    __shared__ __attribute__((aligned(16))) T smem[C::SMEM_ELEMS];
+    __shared__ __attribute__((aligned(16))) T smem[C::SMEM_ELEMS * KS];
 
     const int tid = threadIdx.x;
-    // wave index as a scalar: loop bounds derived from it stay wave-uniform
-    const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
+    // wave index as a scalar: loop bounds derived from it stay wave-uniform;
+    // w: the wave's 32-query block, sp: its key split
+    const int lane = tid & 63, wg = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
+    const int w = wg & 3, sp = wg >> 2;
 
     const int L = xcd_remap(blockIdx.x, gridDim.x);
     const int bh = L / p.n_qtiles;
@@ -83,6 +91,10 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     // tiles before n_plain need no masking for any wave of the workgroup
     int n_plain = min(n_tiles, p.Sk / BN);
     if (CAUSAL) n_plain = min(n_plain, (q0 + 1) / BN);
+    // this split walks key tiles sp, sp + KS, ...: local tile j is key tile
+    // j * KS + sp, and lc(n) counts the local tiles among the first n
+    auto lc = [&](int n) { return n > sp ? (n - sp + KS - 1) / KS : 0; };
+    auto key0 = [&](int j) { return (j * KS + sp) * BN; };
 
     // ---- Q into registers (MFMA B operand) ----
     constexpr int QR = C::F32 ? D / 8 : D / 16;  // 16-byte registers per lane
@@ -155,8 +167,8 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
         }
     };
 
-    T* Ks0 = smem;
-    T* Vs0 = smem + 2 * C::KTILE;
+    T* Ks0 = smem + sp * C::SMEM_ELEMS;
+    T* Vs0 = Ks0 + 2 * C::KTILE;
     // K and V tiles go global -> LDS directly and stay row-major.
     // Loads past the last key read as zeros (buffer range check), so the
     // pipeline below issues them unconditionally; such tiles are never used.
@@ -166,18 +178,20 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     // 16-bit tiles: copies the compiler does not track, which it would
     // otherwise make the next LDS read wait for (sync_tiles waits for them)
     auto dma_k = [&](int j, int slot) {
+        const int k0 = key0(j);
         if constexpr (C::F32)
-            kdma.load(kbase + (int64_t)(j * BN) * p.k_ss, p.k_ss, p.Sk - j * BN, Ks0 + slot * C::KTILE, lane);
+            kdma.load(kbase + (int64_t)k0 * p.k_ss, p.k_ss, p.Sk - k0, Ks0 + slot * C::KTILE, lane);
         else
-            kdma.load_untracked(kbase + (int64_t)(j * BN) * p.k_ss, p.k_ss, p.Sk - j * BN, Ks0 + slot * C::KTILE, lane);
+            kdma.load_untracked(kbase + (int64_t)k0 * p.k_ss, p.k_ss, p.Sk - k0, Ks0 + slot * C::KTILE, lane);
     };
     DmaTile<T, BN, D, VW, C::NW> vst;
     vst.init(p.v_ss, lane, wv);
     auto load_v = [&](int j, int slot) {
+        const int k0 = key0(j);
         if constexpr (C::F32)
-            vst.load(vbase + (int64_t)(j * BN) * p.v_ss, p.v_ss, p.Sk - j * BN, Vs0 + slot * C::VTILE, lane);
+            vst.load(vbase + (int64_t)k0 * p.v_ss, p.v_ss, p.Sk - k0, Vs0 + slot * C::VTILE, lane);
         else
-            vst.load_untracked(vbase + (int64_t)(j * BN) * p.v_ss, p.v_ss, p.Sk - j * BN, Vs0 + slot * C::VTILE, lane);
+            vst.load_untracked(vbase + (int64_t)k0 * p.v_ss, p.v_ss, p.Sk - k0, Vs0 + slot * C::VTILE, lane);
     };
 
     // ---- S^T = K Q^T for one key tile ----
@@ -313,9 +327,14 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
     // against the wave's own LDS reads.
     //
     // Waves whose queries all precede a key tile (causal) skip it; tiles
-    // before n_plain need no mask for any wave of the workgroup.
+    // before n_plain need no mask for any wave of the workgroup.  Counts from
+    // here on are of this split's local tiles.
     int n_w = n_tiles;
     if (CAUSAL) n_w = min(n_tiles, (qw0 + 31) / BN + 1);
+    const int n_iter = (n_tiles + KS - 1) / KS;  // local tiles of split 0, the most of any split
+    n_w = lc(n_w);
+    n_plain = lc(n_plain);
+    const int n_tl = lc(n_tiles);
     f32x16 sa[NB], sb[NB];
     s16x8 pk[NPK];
     uint32_t wa[NB], wb[NB];  // keep words of the current / next tile (DROPOUT == 2)
@@ -324,18 +343,18 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
         wait_vmem();
         lds_barrier();
     };
-    if (n_tiles > 0) {
+    if (n_tl > 0) {
         dma_k(0, 0);
         dma_k(1, 1);
         load_v(0, 0);
     }
     sync_tiles();
     if (n_w > 0) {
-        load_bias(0, std::true_type{});
-        load_kb(0, wa);
+        load_bias(key0(0), std::true_type{});
+        load_kb(key0(0), wa);
         qk(Ks0, sa);
         add_bias(sa);
-        if (n_plain == 0) mask(sa, 0);
+        if (n_plain == 0) mask(sa, key0(0));
         update_max(sa);
     }
 
@@ -349,16 +368,16 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
         const bool next = !MASK || j + 1 < n_w;
         if (act) {
             if (next) {
-                load_bias((j + 1) * BN, mask_tag);
-                load_kb((j + 1) * BN, wn);
+                load_bias(key0(j + 1), mask_tag);
+                load_kb(key0(j + 1), wn);
                 qk(Ks0 + ((j + 1) & 1) * C::KTILE, sn);
             }
-            softmax(sc, pk, j * BN, wc);
+            softmax(sc, pk, key0(j), wc);
         }
         if (act) pv(Vs0 + (j & 1) * C::VTILE, sc, pk);
         if (act && next) {
             add_bias(sn);
-            if (MASK) mask(sn, (j + 1) * BN);
+            if (MASK) mask(sn, key0(j + 1));
             update_max(sn);
         }
     };
@@ -380,23 +399,69 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
             wa[blk] = wb[blk];
         }
     }
-    for (; j + 1 < n_tiles; j += 2) {
+    for (; j + 1 < n_tl; j += 2) {
         iter(j, sa, sb, wa, wb, std::true_type{});
         iter(j + 1, sb, sa, wb, wa, std::true_type{});
     }
-    if (j < n_tiles) iter(j, sa, sb, wa, wb, std::true_type{});
+    if (j < n_tl) iter(j, sa, sb, wa, wb, std::true_type{});
+    // splits with fewer tiles pass the barriers of the others' last iteration
+    for (j = n_tl; j < n_iter; ++j) sync_tiles();
+
+    sync_tiles();  // all waves done with the K/V buffers and no copy still in flight
+    if constexpr (KS > 1) {
+        // ---- merge the splits: parts of splits 1.. through LDS into split 0 ----
+        constexpr int NO = (D / 32) * 16;  // O values per lane
+        constexpr int NF = NO + 3;         // + running max, lane-partial sum, raw max
+        static_assert((KS - 1) * 4 * NF * 64 * 4 <= (KS - 1) * C::SMEM_ELEMS * (int)sizeof(T),
+                      "split parts fit the other splits' tile buffers");
+        float* mg = reinterpret_cast<float*>(smem + C::SMEM_ELEMS);
+        auto at = [&](int s2, int f) FA_INLINE { return mg + (((s2 - 1) * 4 + w) * NF + f) * 64 + lane; };
+        if (sp > 0) {
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) *at(sp, 16 * i + r) = o[i][r];
+            *at(sp, NO) = m_run;
+            *at(sp, NO + 1) = l_run;
+            *at(sp, NO + 2) = m_raw;
+        }
+        lds_barrier();
+        if (sp == 0) {
+            float mm = m_run;
+#pragma unroll
+            for (int s2 = 1; s2 < KS; ++s2) mm = fmaxf(mm, *at(s2, NO));
+            const float a0 = fast_exp2(m_run - mm);
+            l_run *= a0;
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[i][r] *= a0;
+#pragma unroll
+            for (int s2 = 1; s2 < KS; ++s2) {
+                const float a = fast_exp2(*at(s2, NO) - mm);
+                l_run = __builtin_fmaf(*at(s2, NO + 1), a, l_run);
+                m_raw = fmaxf(m_raw, *at(s2, NO + 2));
+#pragma unroll
+                for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[i][r] = __builtin_fmaf(*at(s2, 16 * i + r), a, o[i][r]);
+            }
+            m_run = mm;
+        }
+    }
 
     // ---- epilogue: normalise, LSE, stage O^T through LDS, coalesced store ----
+    // (split 0's waves; the others only pass the barriers)
     const float l_tot = pair_sum(l_run);
     const float inv = l_tot > 0.f ? (DROPOUT ? p.rp : 1.f) / l_tot : 0.f;
-    if (hi == 0 && qi < p.Sq) {
+    if (sp == 0 && hi == 0 && qi < p.Sq) {
         const int64_t si = (int64_t)(b * p.H + h) * p.Sq + qi;
         p.lse[si] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
         if (p.mx) p.mx[si] = BIAS ? m_raw : m_raw * p.scale;
     }
-    sync_tiles();  // all waves done with the K/V buffers and no copy still in flight
     constexpr int OW = C::OW;
     T* Os = smem + w * 32 * OW;
+    if (sp == 0) {
 #pragma unroll
     for (int i = 0; i < D / 32; ++i)
 #pragma unroll
@@ -414,18 +479,21 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(const FwdParams p) {
                 *reinterpret_cast<s16x4*>(Os + l32 * OW + d) = v4;
             }
         }
+    }
     lds_barrier();
     constexpr int EPC = 16 / sizeof(T);
     constexpr int CPR = D / EPC;
     T* obase = (T*)p.o + b * p.o_sb + h * p.o_sh;
+    if (sp == 0) {
 #pragma unroll
-    for (int i = 0; i < 32 * CPR / 64; ++i) {
-        const int cidx = lane + 64 * i;
-        const int row = cidx / CPR, col = cidx % CPR;
-        const int q = qw0 + row;
-        if (q < p.Sq)
-            *reinterpret_cast<uint4*>(obase + (int64_t)q * p.o_ss + col * EPC) =
-                *reinterpret_cast<const uint4*>(Os + row * OW + col * EPC);
+        for (int i = 0; i < 32 * CPR / 64; ++i) {
+            const int cidx = lane + 64 * i;
+            const int row = cidx / CPR, col = cidx % CPR;
+            const int q = qw0 + row;
+            if (q < p.Sq)
+                *reinterpret_cast<uint4*>(obase + (int64_t)q * p.o_ss + col * EPC) =
+                    *reinterpret_cast<const uint4*>(Os + row * OW + col * EPC);
+        }
     }
 }
 
@@ -772,7 +840,17 @@ hipError_t launch_fwd_t(const FwdParams& p, hipStream_t s) {
     q.n_qtiles = (p.Sq + C::BM - 1) / C::BM;
     const int64_t nblocks = (int64_t)q.n_qtiles * p.H * p.B;
     if (nblocks <= 0) return hipSuccess;
-    hipLaunchKernelGGL((fwd_kernel<T, D, CAUSAL, DROPOUT, TB>), dim3((unsigned)nblocks), dim3(C::NT), 0, s, q);
+    // grids that leave CUs idle split the key loop inside the workgroup: into
+    // 4 where four splits fit 128 registers a lane without spilling (16-bit,
+    // D = 32, no dropout, no bias), else into 2
+    constexpr int KS_SMALL = (!Elem<T>::kF32 && D == 32 && DROPOUT == 0 && std::is_void<TB>::value) ? 4 : 2;
+    const int n_cu = 256;
+    if (nblocks < n_cu && p.Sk > C::BN) {
+        hipLaunchKernelGGL((fwd_kernel<T, D, CAUSAL, DROPOUT, TB, KS_SMALL>), dim3((unsigned)nblocks),
+                           dim3(C::NT * KS_SMALL), 0, s, q);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL((fwd_kernel<T, D, CAUSAL, DROPOUT, TB, 1>), dim3((unsigned)nblocks), dim3(C::NT), 0, s, q);
     return hipGetLastError();
 }
 
