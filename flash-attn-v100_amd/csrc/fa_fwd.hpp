@@ -71,7 +71,8 @@ __global__ __launch_bounds__(256 * KS, KS == 1 ? 2 : 1) void fwd_kernel(const Fw
     // wave index as a scalar: loop bounds derived from it stay wave-uniform;
     // w: the wave's 32-query block, sp: its key split
     const int lane = tid & 63, wg = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
-    const int w = wg & 3, sp = wg >> 2;
+    // (compile-time 0 without a split: the compiler does not know the block size)
+    const int w = KS == 1 ? wg : wg & 3, sp = KS == 1 ? 0 : wg >> 2;
 
     const int L = xcd_remap(blockIdx.x, gridDim.x);
     const int bh = L / p.n_qtiles;
