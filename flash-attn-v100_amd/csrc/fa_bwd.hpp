@@ -478,6 +478,278 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value && !(Elem<T>::kF32 &&
 }
 
 // ---------------------------------------------------------------------------
+// dK/dV with K and V in LDS (16-bit inputs, D >= 64, no bias, no dropout),
+// for grids of fewer workgroups than CUs.
+// One workgroup = 8 waves = 128 keys of one (batch, KV head), one workgroup per
+// CU.  Waves w and w + 4 share a SIMD and the 32 keys k0 + 32 (w % 4) ..: each
+// takes one of the two 32-query sub-steps of every 64-query tile, and their
+// dK / dV partials are summed through LDS at the end.  With the keys' K and V
+// rows read from LDS (B operands, row reads) instead of held in registers, a
+// wave keeps 64 registers for operand prefetch: the S / dP products and the
+// dV / dK products each run with their LDS reads two steps ahead, as two
+// independent accumulator chains, instead of one MFMA per LDS latency.  Tiles
+// of Q, dO, LSE and delta stream as in dkdv_kernel.
+template <typename T, int D>
+struct Dkdv8Cfg {
+    static constexpr int NW = 8;
+    static constexpr int NT = 64 * NW;
+    static constexpr int BK = 128;                  // keys per workgroup
+    static constexpr int BQ = 64;                   // queries per tile
+    static constexpr int RW = D + (D == 64 ? 8 : 24);  // Q / dO rows, as in DkdvCfg
+    static constexpr int KVW = D + 8;               // K / V rows (conflict-free b128 row reads)
+    static constexpr int QALLOC = BQ * RW * (int)sizeof(T);
+    static constexpr int BUF_BYTES = 2 * QALLOC + 2 * BQ * 4;
+    static constexpr int NBUF = 2;
+    static constexpr int KV_BYTES = BK * KVW * (int)sizeof(T);
+    static constexpr int SMEM_BYTES = 2 * KV_BYTES + NBUF * BUF_BYTES;
+    static constexpr int OW = D + 8;                // output staging stride
+    // waves 4-7 hand their dK, dV (fp32) to waves 0-3 through LDS
+    static constexpr int MERGE_BYTES = 4 * 64 * 2 * (D / 32) * 16 * 4;
+    static_assert(MERGE_BYTES <= SMEM_BYTES && 4 * 32 * OW * (int)sizeof(T) <= SMEM_BYTES, "epilogue fits");
+    static_assert(SMEM_BYTES <= 160 * 1024, "LDS of one CU");
+    using Rows = DmaRowGroups<T, BQ, D, RW, 4>;     // waves 0-3: Q rows, waves 4-7: dO rows
+    using KV = DmaTile<T, BK, D, KVW, NW>;
+};
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void dkdv8_kernel(const BwdParams p, const int n_ktiles) {
+    using C = Dkdv8Cfg<T, D>;
+    static_assert(!Elem<T>::kF32, "16-bit inputs");
+    constexpr int BQ = C::BQ, RW = C::RW, KVW = C::KVW;
+    __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
+    const int kb = w & 3;   // key block
+    const int st = w >> 2;  // query sub-step of every tile
+    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int bhk = L / n_ktiles;
+    const int kt = L - bhk * n_ktiles;
+    const int hk = bhk % p.Hkv, b = bhk / p.Hkv;
+    const int k0 = kt * C::BK;
+    const int kw0 = k0 + 32 * kb;
+    const int kj = kw0 + l32;  // this lane's key
+
+    T* Ks = reinterpret_cast<T*>(smem);
+    T* Vs = reinterpret_cast<T*>(smem + C::KV_BYTES);
+    char* bufs = smem + 2 * C::KV_BYTES;
+    {  // K and V rows of the 128 keys (rows past Sk land as zeros)
+        typename C::KV kd;
+        kd.init(p.k_ss, lane, w);
+        kd.load_untracked((const T*)p.k + b * p.k_sb + (int64_t)k0 * p.k_ss + hk * p.k_sh, p.k_ss, p.Sk - k0, Ks, lane);
+        typename C::KV vd;
+        vd.init(p.v_ss, lane, w);
+        vd.load_untracked((const T*)p.v + b * p.v_sb + (int64_t)k0 * p.v_ss + hk * p.v_sh, p.v_ss, p.Sk - k0, Vs, lane);
+    }
+
+    f32x16 dk[D / 32], dv[D / 32];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) { dk[i] = f32x16{}; dv[i] = f32x16{}; }
+    const float c = p.scale_log2;
+
+    // query tiles as in dkdv_kernel: per query head of the group from the last
+    // one down; the final tiles of each run cross this wave's keys (masked)
+    const int qt_begin = CAUSAL ? (k0 / BQ) : 0;
+    const int qt_end = (p.Sq + BQ - 1) / BQ;
+    const int nq = qt_end > qt_begin ? qt_end - qt_begin : 0;
+    const int total = nq * p.group;
+    const int n_mask = CAUSAL ? min(nq, max(0, (kw0 + 31 + BQ - 1) / BQ - qt_begin)) : 0;
+
+    const bool copy_q = w < 4;
+    typename C::Rows rows;
+    rows.init(copy_q ? p.q_ss : p.do_ss, lane, w & 3);
+    auto buf = [&](int s) -> char* { return bufs + s * C::BUF_BYTES; };
+    auto tile_head = [&](int it) { return hk * p.group + it / nq; };
+    auto tile_q0 = [&](int it) { return (qt_end - 1 - it % nq) * BQ; };
+    auto issue = [&](int it, int s) FA_INLINE {
+        const int hh = tile_head(it), qb0 = tile_q0(it);
+        char* bp = buf(s);
+        const T* src = copy_q ? (const T*)p.q + b * p.q_sb + (int64_t)qb0 * p.q_ss + hh * p.q_sh
+                              : (const T*)p.dout + b * p.do_sb + (int64_t)qb0 * p.do_ss + hh * p.do_sh;
+        rows.load_untracked(src, copy_q ? p.q_ss : p.do_ss, p.Sq - qb0, (const T*)(bp + (copy_q ? 0 : C::QALLOC)));
+        // every wave copies the LSE / delta rows (the same values)
+        const float* wrow = p.lse2 + ((int64_t)b * p.H + hh) * p.ws_stride + qb0;
+        const u32x4 rs = buffer_words(wrow, (p.ws_stride - qb0) * 4);
+        const uint32_t f = lds_addr(bp + 2 * C::QALLOC);
+        dma_load4_untracked(rs, f, 4 * lane);
+        dma_load4_untracked(rs, f + 4 * BQ, 4 * (p.sq_pad + lane));
+    };
+    auto sync_tiles = [&]() {
+        wait_vmem();
+        lds_barrier();
+    };
+
+    // ---- S = Q K^T, dP = dO V^T for this wave's sub-step (C[q][key]) ----
+    // step t: the t-th 16-wide slice of D; reads of step t + 2 during step t
+    constexpr int NK = D / 16;
+    f32x16 sc, dpc;
+    auto sdp = [&](int s) FA_INLINE {
+        const T* Qs = (const T*)buf(s) + (32 * st + l32) * RW + 8 * hi;
+        const T* Ds = (const T*)(buf(s) + C::QALLOC) + (32 * st + l32) * RW + 8 * hi;
+        const T* kr = Ks + (32 * kb + l32) * KVW + 8 * hi;
+        const T* vr = Vs + (32 * kb + l32) * KVW + 8 * hi;
+        s16x8 aq[NK], ak[NK], ad[NK], av[NK];
+        auto rd = [&](int t) FA_INLINE {
+            aq[t] = *reinterpret_cast<const s16x8*>(Qs + 16 * t);
+            ak[t] = *reinterpret_cast<const s16x8*>(kr + 16 * t);
+            ad[t] = *reinterpret_cast<const s16x8*>(Ds + 16 * t);
+            av[t] = *reinterpret_cast<const s16x8*>(vr + 16 * t);
+        };
+        rd(0);
+        rd(1);
+#pragma unroll
+        for (int t = 0; t < NK; ++t) {
+            if (t + 2 < NK) rd(t + 2);
+            sc = Elem<T>::mfma(aq[t], ak[t], t == 0 ? f32x16{} : sc);
+            dpc = Elem<T>::mfma(ad[t], av[t], t == 0 ? f32x16{} : dpc);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+        for (int t = 0; t < NK; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            if (t + 2 < NK) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        }
+    };
+
+    // ---- P and dS (scale applied at the end) ----
+    s16x8 bp8[2], bs8[2];
+    auto softmax_ds = [&](int it, int s, auto mask_tag) FA_INLINE {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const float* lse2 = (const float*)(buf(s) + 2 * C::QALLOC) + 32 * st;
+        const float* dels = lse2 + BQ;
+        const int qb0 = tile_q0(it) + 32 * st;
+        float pd[16], ds[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse2 + 8 * g + 4 * hi);
+            const f32x4 d4 = *reinterpret_cast<const f32x4*>(dels + 8 * g + 4 * hi);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = 4 * g + e;
+                float pv = fast_exp2(__builtin_fmaf(sc[r], c, -l4[e]));
+                if (MASK && qb0 + 8 * g + 4 * hi + e < kj) pv = 0.f;
+                pd[r] = pv;
+                ds[r] = pv * (dpc[r] - d4[e]);
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            bp8[ks] = pack8<T>(pd + 8 * ks);
+            bs8[ks] = pack8<T>(ds + 8 * ks);
+        }
+    };
+
+    // ---- dV^T += dO^T P, dK^T += Q^T dS (A operands by transposing reads) ----
+    auto dkdv_acc = [&](int s) FA_INLINE {
+        const int trow = 4 * hi + ((lane & 15) >> 2);
+        const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+        const T* Qs = (const T*)buf(s) + (32 * st + trow) * RW + tcol;
+        const T* Ds = (const T*)(buf(s) + C::QALLOC) + (32 * st + trow) * RW + tcol;
+        constexpr int NS = 2 * (D / 32);  // steps: (ks, i)
+        s16x8 ad[NS], aq[NS];
+        auto rd = [&](int t) FA_INLINE {
+            const int ks = t / (D / 32), i = t % (D / 32);
+            const int off = 16 * ks * RW + 32 * i;
+            ad[t] = cat4(lds_read_tr16(Ds + off), lds_read_tr16(Ds + off + 8 * RW));
+            aq[t] = cat4(lds_read_tr16(Qs + off), lds_read_tr16(Qs + off + 8 * RW));
+        };
+        rd(0);
+        rd(1);
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+            const int ks = t / (D / 32), i = t % (D / 32);
+            if (t + 2 < NS) rd(t + 2);
+            dv[i] = Elem<T>::mfma(ad[t], bp8[ks], dv[i]);
+            dk[i] = Elem<T>::mfma(aq[t], bs8[ks], dk[i]);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            if (t + 2 < NS) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        }
+    };
+
+    if (total > 0) issue(0, 0);
+    int bcur = 0;
+    auto iter = [&](int it, auto mask_tag) FA_INLINE {
+        sync_tiles();
+        issue(min(it + 1, total - 1), bcur ^ 1);
+        sdp(bcur);
+        softmax_ds(it, bcur, mask_tag);
+        dkdv_acc(bcur);
+        bcur ^= 1;
+    };
+    int it = 0;
+    for (int g = 0; g < p.group; ++g) {
+        for (; it < g * nq + (nq - n_mask); ++it) iter(it, std::false_type{});
+        if (CAUSAL)
+            for (; it < (g + 1) * nq; ++it) iter(it, std::true_type{});
+    }
+
+    // ---- merge: waves 4-7 add their dK, dV into waves 0-3's ----
+    sync_tiles();  // no copy in flight, every wave done with the tiles and K / V
+    float* mg = reinterpret_cast<float*>(smem);
+    constexpr int NV = (D / 32) * 16;
+    if (st == 1) {
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                mg[(kb * 2 * NV + 16 * i + r) * 64 + lane] = dk[i][r];
+                mg[(kb * 2 * NV + NV + 16 * i + r) * 64 + lane] = dv[i][r];
+            }
+    }
+    lds_barrier();
+    if (st == 0) {
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                dk[i][r] += mg[(kb * 2 * NV + 16 * i + r) * 64 + lane];
+                dv[i][r] += mg[(kb * 2 * NV + NV + 16 * i + r) * 64 + lane];
+            }
+    }
+
+    // ---- epilogue (waves 0-3): stage dK^T, dV^T through LDS as rows, coalesced stores ----
+    constexpr int OW = C::OW;
+    constexpr int EPC = 16 / sizeof(T);
+    constexpr int CPR = D / EPC;
+    T* Os = reinterpret_cast<T*>(smem) + kb * 32 * OW;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        lds_barrier();  // the merge reads / the previous pass's stores are done
+        const f32x16* acc = pass == 0 ? dk : dv;
+        const float mul = pass == 0 ? p.scale : 1.f;
+        if (st == 0) {
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    s16x4 v4;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v4[e] = Elem<T>::pack1(acc[i][4 * g + e] * mul);
+                    *reinterpret_cast<s16x4*>(Os + l32 * OW + 32 * i + 8 * g + 4 * hi) = v4;
+                }
+        }
+        lds_barrier();
+        if (st == 0) {
+            T* gbase = pass == 0 ? (T*)p.dk + b * p.dk_sb + hk * p.dk_sh : (T*)p.dv + b * p.dv_sb + hk * p.dv_sh;
+            const int64_t gss = pass == 0 ? p.dk_ss : p.dv_ss;
+#pragma unroll
+            for (int i = 0; i < 32 * CPR / 64; ++i) {
+                const int cidx = lane + 64 * i;
+                const int row = cidx / CPR, col = cidx % CPR;
+                const int key = kw0 + row;
+                if (key < p.Sk)
+                    *reinterpret_cast<uint4*>(gbase + (int64_t)key * gss + col * EPC) =
+                        *reinterpret_cast<const uint4*>(Os + row * OW + col * EPC);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 template <typename T, int D>
 struct DqCfg {
     static constexpr bool F32 = Elem<T>::kF32;
@@ -501,17 +773,23 @@ struct DqCfg {
     static constexpr int MIN_BLOCKS = (F32 && D == 128) ? 1 : 2;
 };
 
-template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
-__global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(const BwdParams p, const int n_qtiles) {
+// KS: key split, as in fwd_kernel: KS groups of 4 waves on the same 128
+// queries, group sp walking key tiles sp, sp + KS, ... through its own LDS
+// buffers; their dQ partials are summed through LDS at the end (small grids).
+template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB, int KS>
+__global__ __launch_bounds__(256 * KS, (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)) void dq_kernel(const BwdParams p,
+                                                                                           const int n_qtiles) {
     using C = DqCfg<T, D>;
     constexpr bool BIAS = !std::is_void<TB>::value;
     using BT = typename std::conditional<BIAS, TB, T>::type;
     constexpr int BN = C::BN, KW = C::KW;
-    __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
+    __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES * KS];
 
     const int tid = threadIdx.x;
     // wave index as a scalar: loop bounds derived from it stay wave-uniform
-    const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
+    const int lane = tid & 63, wg = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
+    // w: the wave's 32-query block, sp: its key split (compile-time 0 without one)
+    const int w = KS == 1 ? wg : wg & 3, sp = KS == 1 ? 0 : wg >> 2;
     const int L = xcd_remap(blockIdx.x, gridDim.x);
     const int bh = L / n_qtiles;
     const int qt = n_qtiles - 1 - (L - bh * n_qtiles);
@@ -551,6 +829,12 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
     const int n_tiles = (kv_end + BN - 1) / BN;
     int n_plain = min(n_tiles, p.Sk / BN);
     if (CAUSAL) n_plain = min(n_plain, (q0 + 1) / BN);
+    // this split's local tile j is key tile j * KS + sp; lc(n) counts its
+    // local tiles among the first n
+    auto lc = [&](int n) { return n > sp ? (n - sp + KS - 1) / KS : 0; };
+    const int n_iter = (n_tiles + KS - 1) / KS;
+    const int n_tl = lc(n_tiles);
+    n_plain = lc(n_plain);
 
     // ---- K / V tiles: waves 0-1 copy K, waves 2-3 copy V, global -> LDS ----
     const T* kbase = (const T*)p.k + b * p.k_sb + hk * p.k_sh;
@@ -558,9 +842,9 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
     const bool copy_k = w < C::NW / 2;
     typename C::Rows rows;
     rows.init(copy_k ? p.k_ss : p.v_ss, lane, w % (C::NW / 2));
-    auto buf = [&](int s) -> char* { return smem + s * C::BUF_BYTES; };
+    auto buf = [&](int s) -> char* { return smem + sp * C::SMEM_BYTES + s * C::BUF_BYTES; };
     auto issue = [&](int j, int s) FA_INLINE {
-        const int k0 = j * BN;
+        const int k0 = (j * KS + sp) * BN;
         const T* src = copy_k ? kbase + (int64_t)k0 * p.k_ss : vbase + (int64_t)k0 * p.v_ss;
         // copies the compiler does not track: it would otherwise make the
         // next LDS read of the current tile wait for them (sync_tiles waits)
@@ -578,7 +862,7 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
     // before the opening barrier.  Past the last tile the copy repeats it
     // (never read), so the copy is branch-free.
     int bcur = 0;
-    if (n_tiles > 0) issue(0, 0);
+    if (n_tl > 0) issue(0, 0);
 
     // bias of this lane's query row (rows past Sq read zeros, keys past Sk read
     // zeros or the next row: both masked)
@@ -689,20 +973,46 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
     };
     auto step = [&](int j, auto mask_tag) FA_INLINE {
         sync_tiles();
-        issue(min(j + 1, n_tiles - 1), bcur ^ 1);
+        issue(min(j + 1, n_tl - 1), bcur ^ 1);
 #pragma unroll
         for (int st = 0; st < C::NSUB; ++st)
-            sub(j * C::BN + 32 * st, (const T*)buf(bcur) + 32 * st * KW, (const T*)(buf(bcur) + C::KALLOC) + 32 * st * KW,
-                mask_tag);
+            sub((j * KS + sp) * C::BN + 32 * st, (const T*)buf(bcur) + 32 * st * KW,
+                (const T*)(buf(bcur) + C::KALLOC) + 32 * st * KW, mask_tag);
         bcur ^= 1;
     };
 
     for (int j = 0; j < n_plain; ++j) step(j, std::false_type{});
-    for (int j = n_plain; j < n_tiles; ++j) step(j, std::true_type{});
+    for (int j = n_plain; j < n_tl; ++j) step(j, std::true_type{});
+    // splits with fewer tiles pass the barriers of the others' last iteration
+    for (int j = n_tl; j < n_iter; ++j) sync_tiles();
 
     sync_tiles();  // no copy in flight, all waves done with the tiles
+    if constexpr (KS > 1) {
+        // ---- sum the splits' dQ into split 0 through LDS ----
+        constexpr int NO = (D / 32) * 16;
+        static_assert((KS - 1) * 4 * NO * 64 * 4 <= (KS - 1) * C::SMEM_BYTES, "parts fit the other splits' buffers");
+        float* mg = reinterpret_cast<float*>(smem + C::SMEM_BYTES);
+        auto at = [&](int s2, int f) FA_INLINE { return mg + (((s2 - 1) * 4 + w) * NO + f) * 64 + lane; };
+        if (sp > 0) {
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) *at(sp, 16 * i + r) = dq[i][r];
+        }
+        lds_barrier();
+        if (sp == 0) {
+#pragma unroll
+            for (int s2 = 1; s2 < KS; ++s2)
+#pragma unroll
+                for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) dq[i][r] += *at(s2, 16 * i + r);
+        }
+    }
+    // ---- epilogue (split 0): stage dQ^T through LDS as rows, coalesced stores ----
     constexpr int OW = C::OW;
     T* Os = (T*)smem + w * 32 * OW;
+    if (sp == 0) {
 #pragma unroll
     for (int i = 0; i < D / 32; ++i)
 #pragma unroll
@@ -720,18 +1030,21 @@ __global__ __launch_bounds__(256, (DqCfg<T, D>::MIN_BLOCKS)) void dq_kernel(cons
                 *reinterpret_cast<s16x4*>(Os + l32 * OW + d) = v4;
             }
         }
+    }
     lds_barrier();
     constexpr int EPC = 16 / sizeof(T);
     constexpr int CPR = D / EPC;
     T* gbase = (T*)p.dq + b * p.dq_sb + h * p.dq_sh;
+    if (sp == 0) {
 #pragma unroll
-    for (int i = 0; i < 32 * CPR / 64; ++i) {
-        const int cidx = lane + 64 * i;
-        const int row = cidx / CPR, col = cidx % CPR;
-        const int q = qw0 + row;
-        if (q < p.Sq)
-            *reinterpret_cast<uint4*>(gbase + (int64_t)q * p.dq_ss + col * EPC) =
-                *reinterpret_cast<const uint4*>(Os + row * OW + col * EPC);
+        for (int i = 0; i < 32 * CPR / 64; ++i) {
+            const int cidx = lane + 64 * i;
+            const int row = cidx / CPR, col = cidx % CPR;
+            const int q = qw0 + row;
+            if (q < p.Sq)
+                *reinterpret_cast<uint4*>(gbase + (int64_t)q * p.dq_ss + col * EPC) =
+                    *reinterpret_cast<const uint4*>(Os + row * OW + col * EPC);
+        }
     }
 }
 
@@ -749,13 +1062,35 @@ hipError_t launch_bwd_t(const BwdParams& p, int stage, hipStream_t s) {
         using C = DkdvCfg<T, D>;
         const int nk = (p.Sk + C::BK - 1) / C::BK;
         const int64_t nb = (int64_t)nk * p.Hkv * p.B;
-        if (nb > 0) hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, DROPOUT, TB>), dim3((unsigned)nb), dim3(C::NT), 0, s, p, nk);
+        bool done = false;
+        if constexpr (!Elem<T>::kF32 && DROPOUT == 0 && std::is_void<TB>::value && D >= 64) {
+            // grids of fewer workgroups than CUs: the 8-wave kernel, whose two
+            // waves per SIMD halve each workgroup's serial tile chain
+            static_assert(Dkdv8Cfg<T, D>::BK == C::BK, "same key blocks");
+            if (nb > 0 && nb < 256) {
+                hipLaunchKernelGGL((dkdv8_kernel<T, D, CAUSAL>), dim3((unsigned)nb), dim3(Dkdv8Cfg<T, D>::NT), 0, s, p, nk);
+                done = true;
+            }
+        }
+        if (!done && nb > 0)
+            hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, DROPOUT, TB>), dim3((unsigned)nb), dim3(C::NT), 0, s, p, nk);
     }
     if (stage < 0 || stage == 2) {
         using C = DqCfg<T, D>;
         const int nq = (p.Sq + C::BM - 1) / C::BM;
         const int64_t nb = (int64_t)nq * p.H * p.B;
-        if (nb > 0) hipLaunchKernelGGL((dq_kernel<T, D, CAUSAL, DROPOUT, TB>), dim3((unsigned)nb), dim3(C::NT), 0, s, p, nq);
+        // grids of fewer workgroups than CUs split the key loop in two inside
+        // the workgroup (as the forward does) where two splits' tiles fit the LDS
+        bool done = false;
+        if constexpr (2 * C::SMEM_BYTES <= 160 * 1024) {
+            if (nb > 0 && nb < 256 && p.Sk > C::BN) {
+                hipLaunchKernelGGL((dq_kernel<T, D, CAUSAL, DROPOUT, TB, 2>), dim3((unsigned)nb), dim3(C::NT * 2), 0, s,
+                                   p, nq);
+                done = true;
+            }
+        }
+        if (!done && nb > 0)
+            hipLaunchKernelGGL((dq_kernel<T, D, CAUSAL, DROPOUT, TB, 1>), dim3((unsigned)nb), dim3(C::NT), 0, s, p, nq);
     }
     return hipGetLastError();
 }
