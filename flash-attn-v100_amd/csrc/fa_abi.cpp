@@ -4,6 +4,7 @@
 // never synchronises.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <mutex>
@@ -475,6 +476,26 @@ int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int
         p.dbias_dtype = a->dbias ? a->dbias_dtype : FA_DTYPE_F32;
         p.dbias_span = a->dbias ? slice_span(a->dbias_stride, a->seqlen_q, a->seqlen_k, p.dbias_es) : 0;
         p.dbias_zero_fill = 1;
+    }
+    // dQ from the stored dS: 16-bit inputs, dS in their dtype or float32, whole
+    // 16-byte chunks (the summed form's float32 parts always qualify: their rows
+    // are Sk rounded up to 4 floats, and the readable span covers whole rows)
+    p.dq_from_ds = 0;
+    p.ds_span = 0;
+    if (a->dbias && a->dtype != FA_DTYPE_F32) {
+        if (reduce_db) {
+            p.dq_from_ds = 1;
+            p.ds_span = (int)std::min<int64_t>((int64_t)a->seqlen_q * dbias_part_row(a->seqlen_k) * 4, 0x7fffffff);
+        } else {
+            const int64_t es = p.dbias_es;
+            const bool chunks = aligned16(a->dbias) && (p.dbias_sb * es) % 16 == 0 && (p.dbias_sh * es) % 16 == 0 &&
+                                (p.dbias_ss * es) % 16 == 0 && ((int64_t)a->seqlen_k * es) % 16 == 0;
+            if (chunks && (es == 4 || a->dbias_dtype == a->dtype)) {
+                p.dq_from_ds = 1;
+                p.ds_span = p.dbias_span;
+                p.dbias_zero_fill = 2;
+            }
+        }
     }
     const bool causal = a->causal != 0;
     const bool dropout = a->dropout_p > 0.f;

@@ -111,7 +111,7 @@ struct DkdvCfg {
 
 // TB: element type of the additive bias (T or float), void = no bias
 template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
-__global__ __launch_bounds__(256, (std::is_void<TB>::value && !(Elem<T>::kF32 && D == 128) ? 2 : 1)) void dkdv_kernel(
+__global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Elem<T>::kF32 && D == 128) ? 2 : 1)) void dkdv_kernel(
     const BwdParams p, const int n_ktiles) {
     using C = DkdvCfg<T, D>;
     constexpr bool BIAS = !std::is_void<TB>::value;
@@ -415,7 +415,7 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value && !(Elem<T>::kF32 &&
     };
     // dBias rows of query tiles the causal loop skips (queries before the first
     // visited tile) are zero; the visited tiles write every other row
-    if (BIAS && CAUSAL && p.dbias != nullptr && p.dbias_zero_fill) {
+    if (BIAS && CAUSAL && p.dbias != nullptr && p.dbias_zero_fill == 1) {
         const int zrows = min(qt_begin * BQ, p.Sq);
         for (int g = 0; g < p.group; ++g) {
             const __amdgpu_buffer_rsrc_t rs = dbias_buf(hk * p.group + g);
@@ -478,8 +478,9 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value && !(Elem<T>::kF32 &&
 }
 
 // ---------------------------------------------------------------------------
-// dK/dV with K and V in LDS (16-bit inputs, D >= 64, no bias, no dropout),
-// for grids of fewer workgroups than CUs.
+// dK/dV with K and V in LDS (16-bit inputs, D >= 64, no dropout): for grids
+// of fewer workgroups than CUs, and with a bias at every grid size (the
+// bias's registers do not fit two workgroups of dkdv_kernel per CU at D = 128).
 // One workgroup = 8 waves = 128 keys of one (batch, KV head), one workgroup per
 // CU.  Waves w and w + 4 share a SIMD and the 32 keys k0 + 32 (w % 4) ..: each
 // takes one of the two 32-query sub-steps of every 64-query tile, and their
@@ -489,6 +490,11 @@ __global__ __launch_bounds__(256, (std::is_void<TB>::value && !(Elem<T>::kF32 &&
 // dV / dK products each run with their LDS reads two steps ahead, as two
 // independent accumulator chains, instead of one MFMA per LDS latency.  Tiles
 // of Q, dO, LSE and delta stream as in dkdv_kernel.
+// With a bias (TB) each wave loads its sub-step's bias values of the next
+// tile once its softmax is done (one set of registers), and the tile barrier
+// waits only for the copies: those loads stay in flight across it.  dBias
+// (= dS) is stored as in dkdv_kernel; the zeros of the causal gradient are
+// written by the dQ pass (dbias_zero_fill == 2) or by the reduction.
 template <typename T, int D>
 struct Dkdv8Cfg {
     static constexpr int NW = 8;
@@ -511,10 +517,12 @@ struct Dkdv8Cfg {
     using KV = DmaTile<T, BK, D, KVW, NW>;
 };
 
-template <typename T, int D, bool CAUSAL>
+template <typename T, int D, bool CAUSAL, typename TB>
 __global__ __launch_bounds__(512, 1) void dkdv8_kernel(const BwdParams p, const int n_ktiles) {
     using C = Dkdv8Cfg<T, D>;
     static_assert(!Elem<T>::kF32, "16-bit inputs");
+    constexpr bool BIAS = !std::is_void<TB>::value;
+    using BT = typename std::conditional<BIAS, TB, T>::type;
     constexpr int BQ = C::BQ, RW = C::RW, KVW = C::KVW;
     __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
 
@@ -578,6 +586,45 @@ __global__ __launch_bounds__(512, 1) void dkdv8_kernel(const BwdParams p, const 
         wait_vmem();
         lds_barrier();
     };
+    // the loop's barrier: the copies of the tile are done once at most the
+    // NBL bias loads issued after them are in flight (vector loads complete in
+    // order; the dBias stores issued between them only add to the count)
+    constexpr int NBL = BIAS ? 16 : 0;
+    auto sync_copies = [&]() {
+        wait_vmem_below<NBL>();
+        barrier_no_fence();
+    };
+
+    // ---- bias of this lane's key for the 16 queries {8 g + 4 hi + e} of the sub-step ----
+    // (as in dkdv_kernel: rows past Sq read zeros, lanes past Sk read zeros or
+    // another row and are never stored; 16-bit values two to a register)
+    constexpr bool B16 = BIAS && !Elem<BT>::kF32;
+    constexpr int NBI = BIAS ? (B16 ? 8 : 16) : 1;
+    using BR = typename std::conditional<B16, s16x2, float>::type;
+    BR braw[NBI];
+    const int bvoff = (4 * hi * (int)p.bias_ss + kj) * (int)sizeof(BT);
+    auto load_bias = [&](int it) FA_INLINE {
+        if constexpr (BIAS) {
+            const __amdgpu_buffer_rsrc_t rs =
+                slice_buffer((const BT*)p.bias + b * p.bias_sb + tile_head(it) * p.bias_sh, p.bias_span);
+            const int qb0 = tile_q0(it) + 32 * st;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const auto x = load_bias1<BT>(rs, bvoff, (qb0 + 8 * (r >> 2) + (r & 3)) * (int)p.bias_ss * (int)sizeof(BT));
+                if constexpr (B16)
+                    braw[r >> 1][r & 1] = x;
+                else
+                    braw[r] = x;
+            }
+        }
+    };
+    auto bias_at = [&](int r) FA_INLINE {
+        if constexpr (B16)
+            return braw[r >> 1][r & 1];
+        else
+            return braw[r];
+    };
+    const int dbvoff = kj < p.Sk ? (4 * hi * (int)p.dbias_ss + kj) * p.dbias_es : kOffNowhere;
 
     // ---- S = Q K^T, dP = dO V^T for this wave's sub-step (C[q][key]) ----
     // step t: the t-th 16-wide slice of D; reads of step t + 2 during step t
@@ -626,11 +673,25 @@ __global__ __launch_bounds__(512, 1) void dkdv8_kernel(const BwdParams p, const 
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int r = 4 * g + e;
-                float pv = fast_exp2(__builtin_fmaf(sc[r], c, -l4[e]));
+                float pv;
+                if constexpr (BIAS)
+                    pv = fast_exp2(__builtin_fmaf(sc[r], c, __builtin_fmaf(bias_f32<BT>(bias_at(r)), kLog2e, -l4[e])));
+                else
+                    pv = fast_exp2(__builtin_fmaf(sc[r], c, -l4[e]));
                 if (MASK && qb0 + 8 * g + 4 * hi + e < kj) pv = 0.f;
                 pd[r] = pv;
                 ds[r] = pv * (dpc[r] - d4[e]);
             }
+        }
+        if (BIAS && p.dbias != nullptr) {
+            const __amdgpu_buffer_rsrc_t dbrs = slice_buffer(
+                (const char*)p.dbias + (b * p.dbias_sb + tile_head(it) * p.dbias_sh) * p.dbias_es, p.dbias_span);
+            with_grad_dtype(p.dbias_dtype, [&](auto dt) FA_INLINE {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    store_grad<decltype(dt)::value>(dbrs, ds[r], dbvoff,
+                                                    (qb0 + 8 * (r >> 2) + (r & 3)) * (int)p.dbias_ss * p.dbias_es);
+            });
         }
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
@@ -670,13 +731,27 @@ __global__ __launch_bounds__(512, 1) void dkdv8_kernel(const BwdParams p, const 
         }
     };
 
-    if (total > 0) issue(0, 0);
+    if (total > 0) {
+        issue(0, 0);
+        load_bias(0);
+    }
     int bcur = 0;
+    // Without a bias the next tile's copy starts right after the barrier.
+    // With one it starts after the softmax, followed by the next bias loads:
+    // the compiler makes the first use of a bias value wait until no vector
+    // load it knows of issued after that value's load is pending (vmcnt(0)),
+    // which would also drain a copy issued before that use.  Past the last
+    // tile the copy and the loads repeat it (never used), which keeps the
+    // count of loads behind the copy fixed.
     auto iter = [&](int it, auto mask_tag) FA_INLINE {
-        sync_tiles();
-        issue(min(it + 1, total - 1), bcur ^ 1);
+        sync_copies();
+        if constexpr (!BIAS) issue(min(it + 1, total - 1), bcur ^ 1);
         sdp(bcur);
         softmax_ds(it, bcur, mask_tag);
+        if constexpr (BIAS) {
+            issue(min(it + 1, total - 1), bcur ^ 1);
+            load_bias(min(it + 1, total - 1));
+        }
         dkdv_acc(bcur);
         bcur ^= 1;
     };
@@ -1049,6 +1124,198 @@ __global__ __launch_bounds__(256 * KS, (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)) 
 }
 
 // ---------------------------------------------------------------------------
+// dQ from the stored dS (16-bit inputs with a bias gradient requested).  The
+// dK/dV pass writes dS = P (dP - delta) of every (query, key) it visits into
+// the gradient buffer (per batch and head; ES bytes per element: the input
+// dtype or float32), which covers every (query, key) this pass reads: a
+// key block of 128 visits the queries from its first key on, and a 128-query
+// tile here reads keys below its end only under the causal mask.  So dQ =
+// scale * dS K is a single product per (batch, head, 128-query tile): dS rows
+// and K rows stream global -> LDS, and no S, P or dP is recomputed.
+// Causal, with dbias_zero_fill == 2, the pass also writes the zeros that no
+// kernel visits: keys from the tile's end (q0 + 128) on, whole row tails.
+template <typename T, int D, int ES>
+struct DqDsCfg {
+    static constexpr int NW = 4;
+    static constexpr int NT = 64 * NW;
+    static constexpr int BM = 32 * NW;                 // queries per workgroup
+    static constexpr int BN = 128 / ES;                // keys per tile: 128 bytes of each dS row
+    static constexpr int KW = D + (D == 64 ? 8 : 24);  // K rows, conflict-free transposing reads (as DqCfg)
+    static constexpr int SW = (128 + 16) / ES;         // dS rows: 144 bytes (conflict-free b128 row reads)
+    using TS = typename std::conditional<ES == 4, float, T>::type;
+    using KRows = DmaRowGroups<T, BN, D, KW, NW>;
+    using SRows = DmaTile<TS, BM, BN, SW, NW>;
+    static constexpr int KALLOC = BN * KW * (int)sizeof(T);
+    static constexpr int BUF_BYTES = KALLOC + BM * SW * ES;
+    static constexpr int NBUF = 2;
+    static constexpr int OW = D + 8;
+    static constexpr int STAGE_BYTES = NW * 32 * OW * (int)sizeof(T);
+    static constexpr int SMEM_BYTES = NBUF * BUF_BYTES > STAGE_BYTES ? NBUF * BUF_BYTES : STAGE_BYTES;
+    static_assert(2 * SMEM_BYTES <= 160 * 1024, "two workgroups per CU");
+};
+
+template <typename T, int D, bool CAUSAL, int ES>
+__global__ __launch_bounds__(256, 2) void dq_ds_kernel(const BwdParams p, const int n_qtiles) {
+    using C = DqDsCfg<T, D, ES>;
+    using TS = typename C::TS;
+    static_assert(!Elem<T>::kF32, "16-bit inputs");
+    static_assert(C::BM == DkdvCfg<T, D>::BK && C::BM == 128, "dS of the keys below a query tile's end is written");
+    constexpr int BN = C::BN, KW = C::KW, SW = C::SW;
+    __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
+    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = L / n_qtiles;
+    const int qt = n_qtiles - 1 - (L - bh * n_qtiles);
+    const int h = bh % p.H, b = bh / p.H;
+    const int hk = h / p.group;
+    const int q0 = qt * C::BM;
+    const int qw0 = q0 + 32 * w;
+    const int qi = qw0 + l32;
+
+    f32x16 dq[D / 32];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) dq[i] = f32x16{};
+
+    // keys past the tile's last query have dS = 0 under the causal mask
+    int kv_end = p.Sk;
+    if (CAUSAL) kv_end = min(kv_end, q0 + C::BM);
+    const int n_tiles = (kv_end + BN - 1) / BN;
+    // tiles before n_plain need no masking for any row of the workgroup
+    int n_plain = min(n_tiles, p.Sk / BN);
+    if (CAUSAL) n_plain = min(n_plain, (q0 + 1) / BN);
+
+    const T* kbase = (const T*)p.k + b * p.k_sb + hk * p.k_sh;
+    const char* dsb = (const char*)p.dbias + (b * p.dbias_sb + h * p.dbias_sh) * ES;
+    typename C::KRows krows;
+    krows.init(p.k_ss, lane, w);
+    typename C::SRows srows;
+    srows.init(p.dbias_ss, lane, w);
+    auto buf = [&](int s) -> char* { return smem + s * C::BUF_BYTES; };
+    // tile j: K rows k0.., dS rows q0.. of keys k0.. (the descriptor's range
+    // stops at the slice's readable end: rows past Sq land as zeros)
+    auto issue = [&](int j, int s) FA_INLINE {
+        const int k0 = j * BN;
+        krows.load_untracked(kbase + (int64_t)k0 * p.k_ss, p.k_ss, p.Sk - k0, (const T*)buf(s));
+        const int64_t toff = ((int64_t)q0 * p.dbias_ss + k0) * ES;
+        const int64_t tlen = ((int64_t)(C::BM - 1) * p.dbias_ss + BN) * ES;
+        const int bytes = (int)max((int64_t)0, min(tlen, (int64_t)p.ds_span - toff));
+        srows.load_words(buffer_words(dsb + toff, bytes), (const TS*)(buf(s) + C::KALLOC));
+    };
+    auto sync_tiles = [&]() {
+        wait_vmem();
+        lds_barrier();
+    };
+
+    // ---- dQ^T += K^T dS^T for the tile in buffer s, 16 keys per step ----
+    // lane (d, h) takes keys 16 ks + {4 h .. 4 h + 3, 8 + 4 h .. 8 + 4 h + 3},
+    // the order of dq_kernel's products (the same sums, term by term): K^T by
+    // two transposing reads of four K rows each, dS^T as two runs of four
+    // elements of its query row
+    const int trow = 4 * hi + ((lane & 15) >> 2);
+    const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    // keys of this lane's row at or past lim are zero (past Sk, or past the query)
+    const int lim = CAUSAL ? min(p.Sk, qi + 1) : p.Sk;
+    auto tile = [&](int j, int s, auto mask_tag) FA_INLINE {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const int k0 = j * BN;
+        if (MASK && CAUSAL && k0 > qw0 + 31) return;  // the wave's rows see none of these keys
+        const T* Ks = (const T*)buf(s);
+        const char* Ss = buf(s) + C::KALLOC + (32 * w + l32) * SW * ES;
+#pragma unroll
+        for (int ks = 0; ks < BN / 16; ++ks) {
+            const int kl = 16 * ks + 4 * hi;  // tile-relative keys kl + 0..3 and kl + 8 + 0..3
+            auto key = [&](int e) { return k0 + kl + (e < 4 ? e : 4 + e); };
+            s16x8 bs;
+            if constexpr (ES == 2) {
+                bs = cat4(*reinterpret_cast<const s16x4*>(Ss + 2 * kl), *reinterpret_cast<const s16x4*>(Ss + 2 * kl + 16));
+                if (MASK) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (key(e) >= lim) bs[e] = 0;
+                }
+            } else {
+                const f32x4 x0 = *reinterpret_cast<const f32x4*>(Ss + 4 * kl);
+                const f32x4 x1 = *reinterpret_cast<const f32x4*>(Ss + 4 * kl + 32);
+                float t8[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    t8[e] = x0[e];
+                    t8[4 + e] = x1[e];
+                }
+                if (MASK) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (key(e) >= lim) t8[e] = 0.f;
+                }
+                bs = pack8<T>(t8);
+            }
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i) {
+                const T* kp = Ks + (16 * ks + trow) * KW + 32 * i + tcol;
+                const s16x8 a = cat4(lds_read_tr16(kp), lds_read_tr16(kp + 8 * KW));
+                dq[i] = Elem<T>::mfma(a, bs, dq[i]);
+            }
+        }
+    };
+
+    // two LDS buffers alternate: tile j is read from buffer j & 1 while tile
+    // j + 1 is copied into the other one (last read in iteration j - 1, which
+    // every wave finished before the opening barrier)
+    int bcur = 0;
+    if (n_tiles > 0) issue(0, 0);
+    auto step = [&](int j, auto mask_tag) FA_INLINE {
+        sync_tiles();
+        if (j + 1 < n_tiles) issue(j + 1, bcur ^ 1);
+        tile(j, bcur, mask_tag);
+        bcur ^= 1;
+    };
+    for (int j = 0; j < n_plain; ++j) step(j, std::false_type{});
+    for (int j = n_plain; j < n_tiles; ++j) step(j, std::true_type{});
+    sync_tiles();  // every wave done with the tiles
+
+    // ---- epilogue: stage dQ^T through LDS as rows, coalesced stores ----
+    constexpr int OW = C::OW;
+    T* Os = (T*)smem + w * 32 * OW;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            s16x4 v4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v4[e] = Elem<T>::pack1(dq[i][4 * g + e] * p.scale);
+            *reinterpret_cast<s16x4*>(Os + l32 * OW + 32 * i + 8 * g + 4 * hi) = v4;
+        }
+    lds_barrier();
+    constexpr int EPC = 16 / sizeof(T);
+    constexpr int CPR = D / EPC;
+    T* gbase = (T*)p.dq + b * p.dq_sb + h * p.dq_sh;
+#pragma unroll
+    for (int i = 0; i < 32 * CPR / 64; ++i) {
+        const int cidx = lane + 64 * i;
+        const int row = cidx / CPR, col = cidx % CPR;
+        const int q = qw0 + row;
+        if (q < p.Sq)
+            *reinterpret_cast<uint4*>(gbase + (int64_t)q * p.dq_ss + col * EPC) =
+                *reinterpret_cast<const uint4*>(Os + row * OW + col * EPC);
+    }
+
+    // ---- zeros of the gradient no kernel visits: keys from q0 + 128 on ----
+    if (CAUSAL && p.dbias_zero_fill == 2) {
+        const int kz = q0 + C::BM;
+        const int nrow = min(C::BM, p.Sq - q0);
+        if (kz < p.Sk) {
+            const int cpr = (p.Sk - kz) * ES / 16;  // 16-byte chunks per row tail
+            char* zb = (char*)p.dbias + (b * p.dbias_sb + h * p.dbias_sh + (int64_t)q0 * p.dbias_ss + kz) * ES;
+            for (int r = w; r < nrow; r += C::NW)
+                for (int c = lane; c < cpr; c += 64)
+                    *reinterpret_cast<uint4*>(zb + (int64_t)r * p.dbias_ss * ES + 16 * c) = make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
 hipError_t launch_bwd_t(const BwdParams& p, int stage, hipStream_t s) {
     if (stage < 0 || stage == 0) {
@@ -1063,12 +1330,17 @@ hipError_t launch_bwd_t(const BwdParams& p, int stage, hipStream_t s) {
         const int nk = (p.Sk + C::BK - 1) / C::BK;
         const int64_t nb = (int64_t)nk * p.Hkv * p.B;
         bool done = false;
-        if constexpr (!Elem<T>::kF32 && DROPOUT == 0 && std::is_void<TB>::value && D >= 64) {
+        if constexpr (!Elem<T>::kF32 && DROPOUT == 0 && D >= 64) {
             // grids of fewer workgroups than CUs: the 8-wave kernel, whose two
-            // waves per SIMD halve each workgroup's serial tile chain
+            // waves per SIMD halve each workgroup's serial tile chain; with a
+            // bias at every grid size (two waves per SIMD where dkdv_kernel
+            // fits one), unless the causal zeros of dBias are its job
             static_assert(Dkdv8Cfg<T, D>::BK == C::BK, "same key blocks");
-            if (nb > 0 && nb < 256) {
-                hipLaunchKernelGGL((dkdv8_kernel<T, D, CAUSAL>), dim3((unsigned)nb), dim3(Dkdv8Cfg<T, D>::NT), 0, s, p, nk);
+            constexpr bool BIAS = !std::is_void<TB>::value;
+            const bool fill = BIAS && CAUSAL && p.dbias != nullptr && p.dbias_zero_fill == 1;
+            if (nb > 0 && (nb < 256 || BIAS) && !fill) {
+                hipLaunchKernelGGL((dkdv8_kernel<T, D, CAUSAL, TB>), dim3((unsigned)nb), dim3(Dkdv8Cfg<T, D>::NT), 0, s, p,
+                                   nk);
                 done = true;
             }
         }
@@ -1079,11 +1351,24 @@ hipError_t launch_bwd_t(const BwdParams& p, int stage, hipStream_t s) {
         using C = DqCfg<T, D>;
         const int nq = (p.Sq + C::BM - 1) / C::BM;
         const int64_t nb = (int64_t)nq * p.H * p.B;
+        bool done = false;
+        // dS stored by the dK/dV pass: dQ = scale * dS K
+        if constexpr (!Elem<T>::kF32 && !std::is_void<TB>::value) {
+            if (p.dq_from_ds) {
+                static_assert(DqDsCfg<T, D, 2>::BM == C::BM && DqDsCfg<T, D, 4>::BM == C::BM, "same query tiles");
+                if (nb > 0) {
+                    if (p.dbias_es == 4)
+                        hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, 4>), dim3((unsigned)nb), dim3(256), 0, s, p, nq);
+                    else
+                        hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, 2>), dim3((unsigned)nb), dim3(256), 0, s, p, nq);
+                }
+                done = true;
+            }
+        }
         // grids of fewer workgroups than CUs split the key loop in two inside
         // the workgroup (as the forward does) where two splits' tiles fit the LDS
-        bool done = false;
         if constexpr (2 * C::SMEM_BYTES <= 160 * 1024) {
-            if (nb > 0 && nb < 256 && p.Sk > C::BN) {
+            if (!done && nb > 0 && nb < 256 && p.Sk > C::BN) {
                 hipLaunchKernelGGL((dq_kernel<T, D, CAUSAL, DROPOUT, TB, 2>), dim3((unsigned)nb), dim3(C::NT * 2), 0, s,
                                    p, nq);
                 done = true;

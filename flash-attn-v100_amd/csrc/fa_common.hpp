@@ -460,8 +460,12 @@ struct DmaTile {
     // the caller waits for it (vmcnt) before the barrier that publishes it
     __device__ FA_INLINE inline void load_untracked(const T* base, int64_t row_stride, int nvalid, const T* lds,
                                                     int lane) const {
+        load_words(row_buffer_words<T, D, R>(base, row_stride, nvalid), lds);
+    }
+    // the same untracked copy through a caller-built descriptor (whose range
+    // ends where the readable data ends; chunks past it land as zeros)
+    __device__ FA_INLINE inline void load_words(const u32x4& rs, const T* lds) const {
         static_assert(CHUNKS % 64 == 0, "whole instructions (an idle lane would need its own exec mask)");
-        const u32x4 rs = row_buffer_words<T, D, R>(base, row_stride, nvalid);
         const uint32_t l0 = lds_addr(lds);
 #pragma unroll
         for (int t = 0; t < PER; ++t) {

@@ -76,7 +76,17 @@ struct BwdParams {
     int dbias_span;    // bytes of one (batch, head) slice
     int dbias_dtype;   // 0 fp16, 1 bf16, 2 fp32 (the FA_DTYPE_* codes)
     int dbias_es;      // its element size in bytes
-    int dbias_zero_fill;  // causal: also zero the rows of query tiles the loop skips
+    // causal: who writes the zeros of the gradient that no kernel visits
+    // (entries above the dK/dV blocks' first query tiles): 0 nobody (the
+    // summed form, whose reduction writes them), 1 the dK/dV kernel, 2 the dQ
+    // pass that reads dS (dq_from_ds)
+    int dbias_zero_fill;
+    // 1: the dQ pass reads dS from dbias (written by the dK/dV pass, dbias_es
+    // bytes per element: the input dtype or float32) instead of recomputing
+    // it; the gradient's base and row / batch / head strides are then 16-byte
+    // aligned and Sk * dbias_es is a multiple of 16
+    int dq_from_ds;
+    int ds_span;  // readable bytes of one (batch, head) dS slice (dq_from_ds)
 };
 
 // Sum of per-(batch, head) dBias slices over broadcast dimensions:

@@ -205,10 +205,12 @@ def test_gradient_checkpointing_recomputes_output(dtype, causal, p, with_bias, H
         runs.append([o.detach(), qq.grad, kk.grad, vv.grad] + ([bb.grad] if with_bias else []))
     for a, b in zip(*runs):
         assert torch.equal(a, b)
-    # the context manager switches it on for calls inside the region
+    # the context manager switches it on for calls inside the region (a bias
+    # that requires grad, as above: dQ is then computed from the stored dS)
     with fa.ops.attention.gradient_checkpointing_mode():
         qq = q.clone().requires_grad_(True)
-        o = fa.flash_attention_v100(qq, k, v, causal=causal, dropout_p=p, bias=bias, dropout_seed=99,
+        bb = bias.clone().requires_grad_(True) if with_bias else None
+        o = fa.flash_attention_v100(qq, k, v, causal=causal, dropout_p=p, bias=bb, dropout_seed=99,
                                     dropout_offset=7)
         assert o.data_ptr() not in {t.data_ptr() for t in o.grad_fn.saved_tensors}
         o.backward(do)
