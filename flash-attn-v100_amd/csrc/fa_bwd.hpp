@@ -1132,8 +1132,10 @@ __global__ __launch_bounds__(256 * KS, (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)) 
 // tile here reads keys below its end only under the causal mask.  So dQ =
 // scale * dS K is a single product per (batch, head, 128-query tile): dS rows
 // and K rows stream global -> LDS, and no S, P or dP is recomputed.
-// Causal, with dbias_zero_fill == 2, the pass also writes the zeros that no
-// kernel visits: keys from the tile's end (q0 + 128) on, whole row tails.
+// Causal, with `fill`, the pass also writes the zeros that no kernel visits:
+// keys from the tile's end (q0 + 128) on, whole row tails.  (Spreading them
+// over the key loop does not overlap them with its reads: the pass is bound
+// by the HBM traffic of both.)
 template <typename T, int D, int ES>
 struct DqDsCfg {
     static constexpr int NW = 4;
@@ -1155,7 +1157,7 @@ struct DqDsCfg {
 };
 
 template <typename T, int D, bool CAUSAL, int ES>
-__global__ __launch_bounds__(256, 2) void dq_ds_kernel(const BwdParams p, const int n_qtiles) {
+__global__ __launch_bounds__(256, 2) void dq_ds_kernel(const BwdParams p, const int n_qtiles, const int fill) {
     using C = DqDsCfg<T, D, ES>;
     using TS = typename C::TS;
     static_assert(!Elem<T>::kF32, "16-bit inputs");
@@ -1302,7 +1304,7 @@ __global__ __launch_bounds__(256, 2) void dq_ds_kernel(const BwdParams p, const 
     }
 
     // ---- zeros of the gradient no kernel visits: keys from q0 + 128 on ----
-    if (CAUSAL && p.dbias_zero_fill == 2) {
+    if (CAUSAL && fill) {
         const int kz = q0 + C::BM;
         const int nrow = min(C::BM, p.Sq - q0);
         if (kz < p.Sk) {
@@ -1316,6 +1318,22 @@ __global__ __launch_bounds__(256, 2) void dq_ds_kernel(const BwdParams p, const 
 }
 
 // ---------------------------------------------------------------------------
+// Whether the dK/dV stage runs dkdv8_kernel (16-bit inputs, no dropout, D >=
+// 64): on grids of fewer workgroups than CUs, whose serial tile chain its two
+// waves per SIMD halve, and with a bias at every grid size (two waves per SIMD
+// where dkdv_kernel fits one), unless dkdv_kernel's per-element zero fill of
+// the causal dBias is needed (rows not 16-byte aligned).
+template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
+inline bool dkdv8_runs(const BwdParams& p) {
+    if constexpr (!Elem<T>::kF32 && DROPOUT == 0 && D >= 64) {
+        constexpr bool BIAS = !std::is_void<TB>::value;
+        const int64_t nb = (int64_t)((p.Sk + DkdvCfg<T, D>::BK - 1) / DkdvCfg<T, D>::BK) * p.Hkv * p.B;
+        const bool fill1 = BIAS && CAUSAL && p.dbias != nullptr && p.dbias_zero_fill == 1;
+        return nb > 0 && (nb < 256 || BIAS) && !fill1;
+    }
+    return false;
+}
+
 template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
 hipError_t launch_bwd_t(const BwdParams& p, int stage, hipStream_t s) {
     if (stage < 0 || stage == 0) {
@@ -1331,14 +1349,8 @@ hipError_t launch_bwd_t(const BwdParams& p, int stage, hipStream_t s) {
         const int64_t nb = (int64_t)nk * p.Hkv * p.B;
         bool done = false;
         if constexpr (!Elem<T>::kF32 && DROPOUT == 0 && D >= 64) {
-            // grids of fewer workgroups than CUs: the 8-wave kernel, whose two
-            // waves per SIMD halve each workgroup's serial tile chain; with a
-            // bias at every grid size (two waves per SIMD where dkdv_kernel
-            // fits one), unless the causal zeros of dBias are its job
             static_assert(Dkdv8Cfg<T, D>::BK == C::BK, "same key blocks");
-            constexpr bool BIAS = !std::is_void<TB>::value;
-            const bool fill = BIAS && CAUSAL && p.dbias != nullptr && p.dbias_zero_fill == 1;
-            if (nb > 0 && (nb < 256 || BIAS) && !fill) {
+            if (dkdv8_runs<T, D, CAUSAL, DROPOUT, TB>(p)) {
                 hipLaunchKernelGGL((dkdv8_kernel<T, D, CAUSAL, TB>), dim3((unsigned)nb), dim3(Dkdv8Cfg<T, D>::NT), 0, s, p,
                                    nk);
                 done = true;
@@ -1356,11 +1368,12 @@ hipError_t launch_bwd_t(const BwdParams& p, int stage, hipStream_t s) {
         if constexpr (!Elem<T>::kF32 && !std::is_void<TB>::value) {
             if (p.dq_from_ds) {
                 static_assert(DqDsCfg<T, D, 2>::BM == C::BM && DqDsCfg<T, D, 4>::BM == C::BM, "same query tiles");
+                const int fill = p.dbias_zero_fill == 2;
                 if (nb > 0) {
                     if (p.dbias_es == 4)
-                        hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, 4>), dim3((unsigned)nb), dim3(256), 0, s, p, nq);
+                        hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, 4>), dim3((unsigned)nb), dim3(256), 0, s, p, nq, fill);
                     else
-                        hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, 2>), dim3((unsigned)nb), dim3(256), 0, s, p, nq);
+                        hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, 2>), dim3((unsigned)nb), dim3(256), 0, s, p, nq, fill);
                 }
                 done = true;
             }

@@ -59,35 +59,47 @@ struct FwdCfg {
 // merged through LDS at the end (exactly: each part is rescaled to the common
 // maximum).  Small grids use it: a workgroup's key loop is a serial chain of
 // tile latencies, and KS groups walk it KS times shorter on the same CU.
-template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB, int KS>
-__global__ __launch_bounds__(256 * KS, KS == 1 ? 2 : 1) void fwd_kernel(const FwdParams p) {
+// QG: query groups.  With QG = 2 (16-bit inputs and bias, no dropout, no key
+// split) the workgroup has 2 groups of 4 waves on 256 queries, which share
+// the K/V tiles, and each wave stages its bias rows through a private LDS
+// region: 16-byte copies along the rows, where per-lane loads (one query row
+// per lane) touch 32 rows per instruction.  The LDS of one such workgroup
+// holds the K/V tiles and the 8 bias regions.
+template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB, int KS, int QG = 1>
+__global__ __launch_bounds__(256 * KS * QG, KS == 1 && QG == 1 ? 2 : 1) void fwd_kernel(const FwdParams p) {
     using C = FwdCfg<T, D>;
     constexpr bool BIAS = !std::is_void<TB>::value;
     using BT = typename std::conditional<BIAS, TB, T>::type;
     constexpr int BN = C::BN, NB = C::NB, KW = C::KW, VW = C::VW;
-    __shared__ __attribute__((aligned(16))) T smem[C::SMEM_ELEMS * KS];
+    constexpr bool BIAS_LDS = QG > 1;
+    static_assert(QG == 1 || (QG == 2 && BIAS && !Elem<BT>::kF32 && !C::F32 && DROPOUT == 0 && KS == 1 && BN == 64),
+                  "query groups: the staged 16-bit bias path");
+    constexpr int BREG = 32 * 64;  // elements of a wave's bias region (32 rows of 64 keys)
+    __shared__ __attribute__((aligned(16))) T smem[C::SMEM_ELEMS * KS + (BIAS_LDS ? 4 * QG * BREG : 0)];
 
     const int tid = threadIdx.x;
     // wave index as a scalar: loop bounds derived from it stay wave-uniform;
     // w: the wave's 32-query block, sp: its key split
     const int lane = tid & 63, wg = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
-    // (compile-time 0 without a split: the compiler does not know the block size)
-    const int w = KS == 1 ? wg : wg & 3, sp = KS == 1 ? 0 : wg >> 2;
+    // (compile-time 0 without a split: the compiler does not know the block
+    // size); qg: the wave's query group
+    const int w = KS == 1 && QG == 1 ? wg : wg & 3, sp = KS == 1 ? 0 : wg >> 2;
+    const int qg = QG == 1 ? 0 : wg >> 2;
 
     const int L = xcd_remap(blockIdx.x, gridDim.x);
     const int bh = L / p.n_qtiles;
     const int qt = p.n_qtiles - 1 - (L - bh * p.n_qtiles);  // longest causal rows first
     const int h = bh % p.H, b = bh / p.H;
     const int hk = h / p.group;
-    const int q0 = qt * C::BM;
-    const int qw0 = q0 + 32 * w;
+    const int q0 = qt * C::BM * QG;  // the workgroup's first query
+    const int qw0 = q0 + C::BM * qg + 32 * w;
     const int qi = qw0 + l32;
 
     const T* __restrict__ kbase = (const T*)p.k + b * p.k_sb + hk * p.k_sh;
     const T* __restrict__ vbase = (const T*)p.v + b * p.v_sb + hk * p.v_sh;
 
     int kv_end = p.Sk;
-    if (CAUSAL) kv_end = min(kv_end, min(q0 + C::BM, p.Sq));
+    if (CAUSAL) kv_end = min(kv_end, min(q0 + C::BM * QG, p.Sq));
     const int n_tiles = (kv_end + BN - 1) / BN;
     // tiles before n_plain need no masking for any wave of the workgroup
     int n_plain = min(n_tiles, p.Sk / BN);
@@ -128,9 +140,24 @@ __global__ __launch_bounds__(256 * KS, KS == 1 ? 2 : 1) void fwd_kernel(const Fw
     const __amdgpu_buffer_rsrc_t brs =
         slice_buffer((const BT*)p.bias + b * p.bias_sb + h * p.bias_sh, BIAS ? p.bias_span : 0);
     const int bvoff = (qi * (int)p.bias_ss + 4 * hi) * (int)sizeof(BT);
+    // staged bias (BIAS_LDS): copy chunk 64 t + lane of the wave's region is row
+    // 8 t + lane / 8 at chunk position lane % 8, which holds key chunk
+    // (lane % 8) ^ (lane / 8) of the row (keys 8 c .. 8 c + 7 of chunk c); rows
+    // read 32 at one key chunk then fall in 8 distinct chunk positions.  Bias
+    // rows are whole 16-byte chunks here (Sk % 8 == 0), so no copy straddles
+    // the end of the slice.
+    T* const bsm = smem + C::SMEM_ELEMS * KS + (BIAS_LDS ? wg * BREG : 0);
+    const u32x4 bwords = buffer_words((const BT*)p.bias + b * p.bias_sb + h * p.bias_sh, BIAS_LDS ? p.bias_span : 0);
+    const int bdoff = ((qw0 + (lane >> 3)) * (int)p.bias_ss + 8 * ((lane & 7) ^ (lane >> 3))) * (int)sizeof(BT);
     // a tile of plain iterations is always whole (MAYBE_TAIL = false)
     auto load_bias = [&](int k0, auto tail_tag) FA_INLINE {
-        if constexpr (BIAS) {
+        if constexpr (BIAS_LDS) {
+            // the region was last read by this wave's add_bias of the previous tile
+            const uint32_t l0 = lds_addr(bsm);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                dma_load16_untracked(bwords, l0 + 1024 * t, bdoff + (8 * t * (int)p.bias_ss + k0) * (int)sizeof(BT));
+        } else if constexpr (BIAS) {
             auto load_all = [&](auto full_tag) FA_INLINE {
 #pragma unroll
                 for (int g = 0; g < NG; ++g)
@@ -145,7 +172,20 @@ __global__ __launch_bounds__(256 * KS, KS == 1 ? 2 : 1) void fwd_kernel(const Fw
     };
     // t = S * scale + bias
     auto add_bias = [&](f32x16 (&s)[NB]) FA_INLINE {
-        if constexpr (BIAS) {
+        if constexpr (BIAS_LDS) {
+            wait_vmem();  // the wave's staged bias (and the tile copies issued before it)
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int c = 4 * blk + g;  // key chunk of registers 4 g .. 4 g + 3
+                    const s16x4 v = *reinterpret_cast<const s16x4*>(bsm + l32 * 64 + 8 * (c ^ (l32 & 7)) + 4 * hi);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        s[blk][4 * g + e] = __builtin_fmaf(s[blk][4 * g + e], p.scale, bias_f32<BT>(v[e]));
+                }
+        } else if constexpr (BIAS) {
 #pragma unroll
             for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
@@ -173,8 +213,8 @@ __global__ __launch_bounds__(256 * KS, KS == 1 ? 2 : 1) void fwd_kernel(const Fw
     // K and V tiles go global -> LDS directly and stay row-major.
     // Loads past the last key read as zeros (buffer range check), so the
     // pipeline below issues them unconditionally; such tiles are never used.
-    const int wv = __builtin_amdgcn_readfirstlane(w);
-    DmaTile<T, BN, D, KW, C::NW> kdma;
+    const int wv = __builtin_amdgcn_readfirstlane(QG > 1 ? wg : w);
+    DmaTile<T, BN, D, KW, C::NW * QG> kdma;
     kdma.init(p.k_ss, lane, wv);
     // 16-bit tiles: copies the compiler does not track, which it would
     // otherwise make the next LDS read wait for (sync_tiles waits for them)
@@ -185,7 +225,7 @@ __global__ __launch_bounds__(256 * KS, KS == 1 ? 2 : 1) void fwd_kernel(const Fw
         else
             kdma.load_untracked(kbase + (int64_t)k0 * p.k_ss, p.k_ss, p.Sk - k0, Ks0 + slot * C::KTILE, lane);
     };
-    DmaTile<T, BN, D, VW, C::NW> vst;
+    DmaTile<T, BN, D, VW, C::NW * QG> vst;
     vst.init(p.v_ss, lane, wv);
     auto load_v = [&](int j, int slot) {
         const int k0 = key0(j);
@@ -461,7 +501,8 @@ __global__ __launch_bounds__(256 * KS, KS == 1 ? 2 : 1) void fwd_kernel(const Fw
         if (p.mx) p.mx[si] = BIAS ? m_raw : m_raw * p.scale;
     }
     constexpr int OW = C::OW;
-    T* Os = smem + w * 32 * OW;
+    static_assert(C::NW * QG * 32 * OW <= C::SMEM_ELEMS, "O staging of every wave fits the K/V buffers");
+    T* Os = smem + (QG > 1 ? wg : w) * 32 * OW;
     if (sp == 0) {
 #pragma unroll
     for (int i = 0; i < D / 32; ++i)
@@ -837,6 +878,20 @@ hipError_t launch_fwd_t(const FwdParams& p, hipStream_t s) {
         }
     }
     using C = FwdCfg<T, D>;
+    // a 16-bit bias without dropout: 256-query workgroups that stage the bias
+    // through LDS, where the grid still fills the CUs and bias rows are whole
+    // 16-byte chunks
+    if constexpr (!Elem<T>::kF32 && DROPOUT == 0 && !std::is_void<TB>::value) {
+        if constexpr (!Elem<TB>::kF32) {
+            FwdParams q = p;
+            q.n_qtiles = (p.Sq + 2 * C::BM - 1) / (2 * C::BM);
+            const int64_t nb2 = (int64_t)q.n_qtiles * p.H * p.B;
+            if (nb2 >= 256 && p.Sk % 8 == 0) {
+                hipLaunchKernelGGL((fwd_kernel<T, D, CAUSAL, 0, TB, 1, 2>), dim3((unsigned)nb2), dim3(C::NT * 2), 0, s, q);
+                return hipGetLastError();
+            }
+        }
+    }
     FwdParams q = p;
     q.n_qtiles = (p.Sq + C::BM - 1) / C::BM;
     const int64_t nblocks = (int64_t)q.n_qtiles * p.H * p.B;

@@ -78,8 +78,8 @@ struct BwdParams {
     int dbias_es;      // its element size in bytes
     // causal: who writes the zeros of the gradient that no kernel visits
     // (entries above the dK/dV blocks' first query tiles): 0 nobody (the
-    // summed form, whose reduction writes them), 1 the dK/dV kernel, 2 the dQ
-    // pass that reads dS (dq_from_ds)
+    // summed form, whose reduction writes them), 1 dkdv_kernel, element by
+    // element, 2 the dQ pass that reads dS (dq_from_ds), whole row tails
     int dbias_zero_fill;
     // 1: the dQ pass reads dS from dbias (written by the dK/dV pass, dbias_es
     // bytes per element: the input dtype or float32) instead of recomputing
