@@ -176,10 +176,12 @@ ALL_CONFIGS = [
      for d in (32, 64, 128) for dt in ("float32", "float16")]
 
 
-def all_configs(n: int, cpu: bool, cpu_target_s: float = 3.0, only=None):
+def all_configs(n: int, cpu: bool, cpu_target_s: float = 3.0, only=None, warmup: int = 5):
     """One JSON line per benchmark config: GPU time of its pass (HIP events,
-    mean of ``n`` calls) and, unless ``cpu`` is False, the fp32 math path of
-    oracle/ on this host for B=1 and as many heads as fit ``cpu_target_s``."""
+    mean of ``n`` calls after ``warmup`` untimed ones, so that the clock has
+    left the idle state the CPU sample of the previous config put it in) and,
+    unless ``cpu`` is False, the fp32 math path of oracle/ on this host for B=1
+    and as many heads as fit ``cpu_target_s``."""
     import ctypes
 
     import torch
@@ -191,7 +193,8 @@ def all_configs(n: int, cpu: bool, cpu_target_s: float = 3.0, only=None):
     sp = ctypes.c_void_p(stream.cuda_stream)
 
     def timed(fn):
-        fn()
+        for _ in range(max(1, warmup)):
+            fn()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(n):
@@ -344,7 +347,7 @@ def main():
     if a.dbias and a.bias == "none":
         ap.error("--dbias needs --bias")
     if a.all_configs:
-        all_configs(max(a.steps, 10), not a.no_cpu_baseline, only=a.config)
+        all_configs(max(a.steps, 10), not a.no_cpu_baseline, only=a.config, warmup=a.warmup)
         return
     r = gpu_bench(a.steps, a.warmup, a.bias, a.dbias)
     F = f_fwd()
@@ -353,6 +356,14 @@ def main():
     fwd_tflops = F / (r["fwd_ms"] * 1e-3) / 1e12
     kernels = {"fwd_kernel": r["fwd_ms"], "delta_kernel": r["delta_ms"], "dkdv_kernel": r["dkdv_ms"],
                "dq_kernel": r["dq_ms"]}
+    # the kernels each stage launches at this workload (the keys above name the stages)
+    stage_kernels = {"fwd_kernel": "fwd_kernel (128-query workgroups)", "delta_kernel": "delta_kernel",
+                     "dkdv_kernel": "dkdv_kernel", "dq_kernel": "dq_kernel"}
+    if a.bias != "none":
+        stage_kernels["fwd_kernel"] = "fwd_kernel (256-query workgroups, bias staged through LDS)"
+        stage_kernels["dkdv_kernel"] = "dkdv8_kernel" + (" + dbias_reduce_kernel" if a.bias == "heads" and a.dbias else "")
+        stage_kernels["dq_kernel"] = "dq_ds_kernel (dQ = dS K from the stored dS)" if a.dbias else "dq_kernel"
+
     # algorithmic FLOPs per launch: fwd = QK^T + PV; dkdv = 4 of the 5 backward GEMMs
     # (QK^T recompute, dO V^T, P^T dO, dS^T Q); dq = dS K (its S/dP recompute is extra work)
     algo = {"fwd_kernel": F, "dkdv_kernel": 2.0 * F, "dq_kernel": 0.5 * F}
@@ -393,6 +404,7 @@ def main():
         "fwd_tflops": round(fwd_tflops, 2),
         "fwd_pct_peak": round(100 * fwd_tflops / PEAK_BF16_TFLOPS, 2),
         "kernel_ms": {kk: round(vv, 4) for kk, vv in kernels.items()},
+        "stage_kernels": stage_kernels,
         "fwd_bwd_event_ms": round(r["fwd_bwd_ms"], 4),
         "outputs_finite": r["finite"],
         "device": r["device"],
