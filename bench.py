@@ -178,8 +178,9 @@ ALL_CONFIGS = [
 
 def all_configs(n: int, cpu: bool, cpu_target_s: float = 3.0, only=None, warmup: int = 5):
     """One JSON line per benchmark config: GPU time of its pass (HIP events,
-    mean of ``n`` calls after ``warmup`` untimed ones, so that the clock has
-    left the idle state the CPU sample of the previous config put it in) and,
+    mean of ``n`` calls after at least ``warmup`` untimed ones and 0.2 s of
+    work, so that the clock has left the idle state the CPU sample of the
+    previous config put it in) and,
     unless ``cpu`` is False, the fp32 math path of oracle/ on this host for B=1
     and as many heads as fit ``cpu_target_s``."""
     import ctypes
@@ -193,8 +194,15 @@ def all_configs(n: int, cpu: bool, cpu_target_s: float = 3.0, only=None, warmup:
     sp = ctypes.c_void_p(stream.cuda_stream)
 
     def timed(fn):
-        for _ in range(max(1, warmup)):
+        # warm-up: at least `warmup` calls and 0.2 s of back-to-back work (the
+        # clock ramps up over tens of milliseconds of load)
+        t_end = time.perf_counter() + 0.2
+        k = 0
+        while k < max(1, warmup) or time.perf_counter() < t_end:
             fn()
+            k += 1
+            if k % 8 == 0:
+                torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(n):
