@@ -350,6 +350,27 @@ def test_keep_bits_rules():
         _lib._check_keep_bits(_lib.alloc_keep_bits(B, H, S, S + 40, "cpu"), B, H, S, S, torch.device("cpu"))
 
 
+@pytest.mark.parametrize("Sk", [1, 32, 96, 4128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_keep_word_reads_stay_in_the_buffer(Sk, causal):
+    """The keep-word reads of the three kernels, restated: every word index
+    they form stays below B*H*Sq*kb_w, the buffer the host sizes
+    (csrc/fa_fwd.hpp load_kb, csrc/fa_bwd.hpp load_kbits and dq_kernel's
+    per-sub-step read, each guarded by key < Sk and query < Sq)."""
+    B, H, Sq = 1, 1, 70
+    kb_w = (Sk + 31) // 32
+    words = B * H * Sq * kb_w
+    assert _lib.keep_bits_bytes(B, H, Sq, Sk) == 4 * words
+    last = B * H * Sq - 1  # the last (b, h, q) row: its reads end the buffer
+    for k0 in range(0, ((Sk + 63) // 64) * 64, 32):  # every 32-key sub-step of every 64-key tile
+        if causal and k0 > Sq - 1 + 31:  # waves skip sub-steps past their last query
+            continue
+        if k0 < Sk:  # the guard: a sub-step that starts past Sk reads no word
+            assert last * kb_w + (k0 >> 5) < words
+        else:
+            assert last * kb_w + (k0 >> 5) >= words  # what an unguarded read would touch
+
+
 def test_prepare_bias_layout():
     # unaligned rows (Sk = 13 halves = 26 bytes) are copied into 16-byte padded rows
     b = torch.randn(2, 1, 5, 13).to(torch.float16)
