@@ -19,7 +19,8 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfa_gfx950.so")
 ABI_VERSION = 2
-HEAD_DIMS = (32, 64, 128)
+HEAD_DIMS = (32, 64, 128)  # compiled into the kernels
+MAX_HEAD_DIM = HEAD_DIMS[-1]
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
@@ -156,6 +157,27 @@ def _strides(t: torch.Tensor):
     return _I64x4(*t.stride())
 
 
+def padded_head_dim(d: int) -> int:
+    """The compiled head dim a head dim of ``d`` (1..MAX_HEAD_DIM) runs at: the
+    smallest one >= d.  Zero columns added to q, k and v change no score (the
+    softmax scale is passed explicitly) and make the extra columns of O, dQ,
+    dK and dV exactly zero, so the results at d are those of a kernel built
+    for d; the dropout stream depends on (b, h, query, key) only, so the mask
+    is the same too.  0 for head dims with no kernel."""
+    for hd in HEAD_DIMS:
+        if 0 < d <= hd:
+            return hd
+    return 0
+
+
+def _pad_d(t: torch.Tensor, dp: int) -> torch.Tensor:
+    return t if t.shape[-1] == dp else torch.nn.functional.pad(t, (0, dp - t.shape[-1]))
+
+
+def _unpad_d(t: torch.Tensor, d: int) -> torch.Tensor:
+    return t if t.shape[-1] == d else t[..., :d].contiguous()
+
+
 def seed_offset(seed: Optional[int], offset: Optional[int]) -> Tuple[int, int]:
     """Dropout Philox seed/offset; undrawn values come from torch's CPU
     generator (no device synchronisation, reproducible under torch.manual_seed)."""
@@ -269,7 +291,9 @@ def fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: 
     ``keep_bits`` (from :func:`alloc_keep_bits`, with dropout) receives the
     keep mask applied."""
     lib = load()
-    q, k, v = prepare(q), prepare(k), prepare(v)
+    D = q.shape[-1]
+    dp = padded_head_dim(D) or D  # no kernel: the library rejects it
+    q, k, v = (prepare(_pad_d(t, dp)) for t in (q, k, v))
     pb = _as_prepared(bias, q, k)
     B, Sq, H, _ = q.shape
     o = torch.empty_like(q, memory_format=torch.contiguous_format)
@@ -279,7 +303,7 @@ def fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: 
         _check_keep_bits(keep_bits, B, H, Sq, k.shape[1], q.device)
     a = fwd_args(q, k, v, o, lse, mx, causal, scale, dropout_p, seed, offset, pb, keep_bits)
     _check("fa_fwd", lib.fa_fwd(ctypes.byref(a), _stream(q)))
-    return o, lse, mx
+    return _unpad_d(o, D), lse, mx
 
 
 def bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, offset,
@@ -315,7 +339,9 @@ def bwd(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float = 0.0,
     ``keep_bits``: the mask the forward wrote (same seed / offset), read
     instead of regenerating it."""
     lib = load()
-    q, k, v, o, do = (prepare(t) for t in (q, k, v, o, do))
+    D = q.shape[-1]
+    dp = padded_head_dim(D) or D
+    q, k, v, o, do = (prepare(_pad_d(t, dp)) for t in (q, k, v, o, do))
     pb = _as_prepared(bias, q, k)
     if want_dbias and pb is None:
         raise ValueError("want_dbias needs a bias")
@@ -344,6 +370,7 @@ def bwd(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float = 0.0,
     ws_bytes = lib.fa_bwd_workspace_size(ctypes.byref(a))
     ws = torch.empty(max(int(ws_bytes), 256), device=q.device, dtype=torch.uint8)
     _check("fa_bwd", lib.fa_bwd(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(q)))
+    dq, dk, dv = (_unpad_d(t, D) for t in (dq, dk, dv))
     if want_dbias:
         return dq, dk, dv, reduce_dbias(dbias, pb)
     return dq, dk, dv
@@ -355,7 +382,9 @@ def bwd_static(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float
     scratch, no workspace): returns (dq, dk, dv).  Outputs are allocated here
     by torch; the library call itself allocates nothing."""
     lib = load()
-    q, k, v, o, do = (prepare(t) for t in (q, k, v, o, do))
+    D = q.shape[-1]
+    dp = padded_head_dim(D) or D
+    q, k, v, o, do = (prepare(_pad_d(t, dp)) for t in (q, k, v, o, do))
     lse = lse.contiguous()
     dq = torch.empty_like(q, memory_format=torch.contiguous_format)
     dk = torch.empty_like(k, memory_format=torch.contiguous_format)
@@ -364,7 +393,7 @@ def bwd_static(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float
         _check_keep_bits(keep_bits, q.shape[0], q.shape[2], q.shape[1], k.shape[1], q.device)
     a = bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, dropout_p, seed, offset, None, None, keep_bits)
     _check("fa_bwd_static", lib.fa_bwd_static(ctypes.byref(a), _stream(q)))
-    return dq, dk, dv
+    return tuple(_unpad_d(t, D) for t in (dq, dk, dv))
 
 
 def dropout_mask(seed: int, offset: int, B: int, H: int, Sq: int, Sk: int, p: float,

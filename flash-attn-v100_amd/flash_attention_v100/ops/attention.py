@@ -59,8 +59,9 @@ def _check_kernel_inputs(q, k, v, dropout_p):
         raise ValueError(f"dtype must be one of {SUPPORTED_DTYPES} and equal for q, k, v")
     if q.device.type != "cuda" or k.device != q.device or v.device != q.device:
         raise ValueError("Flash Attention requires q, k, v on the same GPU device")
-    if q.shape[-1] not in _lib.HEAD_DIMS:
-        raise NotImplementedError(f"head_dim {q.shape[-1]} is not compiled (supported: {_lib.HEAD_DIMS})")
+    if not _lib.padded_head_dim(q.shape[-1]):
+        raise NotImplementedError(f"head_dim {q.shape[-1]} has no kernel (1..{_lib.MAX_HEAD_DIM}; head dims "
+                                  f"between the compiled {_lib.HEAD_DIMS} run zero-padded to the next one)")
     if k.shape != v.shape or k.shape[0] != q.shape[0] or k.shape[3] != q.shape[3]:
         raise ValueError(f"incompatible shapes q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
     if k.shape[2] == 0 or q.shape[2] % k.shape[2] != 0:
