@@ -87,11 +87,13 @@ def validate_inputs_enhanced(q, k, v, scale=None, bias=None, dropout_p=0.0):
     return q, k, v, scale
 
 
-def _fallback_to_pytorch(q, k, v, scale, causal, dropout_p, bias, return_softmax_lse):
+def _fallback_to_pytorch(q, k, v, scale, causal, dropout_p, bias, return_softmax_lse, dropout_seed=None,
+                         dropout_offset=None):
     """PyTorch math on the tensors' GPU, computed in float32 (reference
     ``interface.py:453-490`` used SDPA).  Returns a real LSE, unlike the
-    reference's zeros.  Dropout here uses torch's RNG, not the kernels' Philox
-    stream."""
+    reference's zeros.  Dropout applies the kernels' Philox mask for the same
+    seed and offset (drawn by the library's mask kernel), so a seed means the
+    same mask on both paths."""
     if q.device.type != "cuda":
         raise ValueError("fallback requires GPU tensors")
     H = q.shape[2]
@@ -108,7 +110,9 @@ def _fallback_to_pytorch(q, k, v, scale, causal, dropout_p, bias, return_softmax
     lse = torch.logsumexp(s, dim=-1)
     p = torch.softmax(s, dim=-1)
     if dropout_p > 0:
-        p = torch.nn.functional.dropout(p, p=dropout_p, training=True)
+        seed, offset = _lib.seed_offset(dropout_seed, dropout_offset)
+        keep = _lib.dropout_mask(seed, offset, s.shape[0], s.shape[1], s.shape[2], s.shape[3], dropout_p, q.device)
+        p = p * keep.to(p.dtype) / (1.0 - dropout_p)
     o = torch.matmul(p, vf).transpose(1, 2).to(q.dtype)
     return (o, lse) if return_softmax_lse else o
 
@@ -160,7 +164,8 @@ def flash_attention_v100(
             raise
         warnings.warn(f"Flash Attention failed ({e}), falling back to PyTorch implementation", UserWarning)
         _Stats.error_recovery_count += 1
-        return _fallback_to_pytorch(q, k, v, scale, causal, dropout_p, bias, return_softmax_lse)
+        return _fallback_to_pytorch(q, k, v, scale, causal, dropout_p, bias, return_softmax_lse, dropout_seed,
+                                    dropout_offset)
 
 
 # Convenience entry points and context managers of the reference

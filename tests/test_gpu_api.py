@@ -161,6 +161,17 @@ def test_kernel_errors_raise_not_fall_back():
         fa.flash_attention_v100(q, k, v, fallback_on_error=False)
 
 
+def test_fallback_dropout_uses_the_kernel_mask():
+    # the fallback applies the kernels' Philox mask for the same seed / offset
+    q, k, v = _qkv((1, 128, 2, 64), torch.float16)
+    out_k = fa.flash_attention_v100(q, k, v, dropout_p=0.2, dropout_seed=5, dropout_offset=0)
+    out_f = fa.interface._fallback_to_pytorch(q, k, v, 64 ** -0.5, False, 0.2, None, False, 5, 0)
+    err = (out_k.float() - out_f.float()).abs().max().item()
+    other = fa.interface._fallback_to_pytorch(q, k, v, 64 ** -0.5, False, 0.2, None, False, 6, 0)
+    say(f"kernel vs fallback, same seed: {err:.3e}; another seed: {(out_k.float() - other.float()).abs().max().item():.3e}")
+    assert err < 5e-3 < (out_k.float() - other.float()).abs().max().item()
+
+
 def test_standalone_forward_backward_and_compare():
     # reference ops/attention.py:464-718: forward only, backward from saved state, report dict
     from flash_attention_v100 import ops
