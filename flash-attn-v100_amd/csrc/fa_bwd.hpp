@@ -1143,7 +1143,7 @@ struct DqDsCfg {
     static constexpr int BM = 32 * NW;                 // queries per workgroup
     static constexpr int BN = 128 / ES;                // keys per tile: 128 bytes of each dS row
     static constexpr int KW = D + (D == 64 ? 8 : 24);  // K rows, conflict-free transposing reads (as DqCfg)
-    static constexpr int SW = (128 + 16) / ES;         // dS rows: 144 bytes (conflict-free b128 row reads)
+    static constexpr int SW = (128 + 16) / ES;         // dS rows: 144 bytes (rows read at one column spread over the banks)
     using TS = typename std::conditional<ES == 4, float, T>::type;
     using KRows = DmaRowGroups<T, BN, D, KW, NW>;
     using SRows = DmaTile<TS, BM, BN, SW, NW>;
