@@ -144,7 +144,8 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
             vreg[i] = ok ? *reinterpret_cast<const uint4*>(vrow + d0) : make_uint4(0u, 0u, 0u, 0u);
         }
     }
-    wait_vmem();
+    // no wait here: the K / V loads stay in flight while the first tile copy
+    // is issued (the loop's first barrier waits for both)
 
     f32x16 dk[D / 32], dv[D / 32];
 #pragma unroll
@@ -890,7 +891,8 @@ __global__ __launch_bounds__(256 * KS, (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)) 
     const int64_t wi = ((int64_t)b * p.H + h) * p.ws_stride + qi;  // qi < sq_pad
     const float lse2 = p.lse2[wi];
     const float del = p.delta[wi];
-    wait_vmem();
+    // no wait here: these loads stay in flight while the first tile copy is
+    // issued (the loop's first barrier waits for both)
     const float c = p.scale_log2;
     uint64_t row_ctr = 0;
     if (DROPOUT) row_ctr = p.offset + ((uint64_t)(b * p.H + h) * (uint64_t)p.Sq + (uint64_t)qi) * (uint64_t)p.Sk;

@@ -121,7 +121,8 @@ __global__ __launch_bounds__(256 * KS * QG, KS == 1 && QG == 1 ? 2 : 1) void fwd
             qreg[i] = qi < p.Sq ? *reinterpret_cast<const uint4*>(qrow + d0) : make_uint4(0u, 0u, 0u, 0u);
         }
     }
-    wait_vmem();
+    // no wait here: the Q loads stay in flight while the first tile copies
+    // are issued (the barrier before the first product waits for both)
 
     f32x16 o[D / 32];
 #pragma unroll
