@@ -196,10 +196,13 @@ int32_t fa_bwd_check(const fa_bwd_args* args, size_t workspace_bytes);
 int32_t fa_bwd(const fa_bwd_args* args, void* workspace, size_t workspace_bytes, void* hip_stream);
 
 /* One stage of fa_bwd: 0 = delta pre-pass (writes the workspace), 1 = dK/dV,
- * 2 = dQ; -1 = all three (same as fa_bwd).  Stages 1 and 2 only read the
- * workspace and are independent of each other, so after stage 0 a caller may
- * run them on two streams.  No reference counterpart (the reference had one
- * fused Triton backward, kernels/backward_kernel.py:17-205). */
+ * 2 = dQ; -1 = all three (same as fa_bwd).  Without a bias gradient, stages 1
+ * and 2 only read the workspace and are independent of each other, so after
+ * stage 0 a caller may run them on two streams.  With one (dbias non-NULL)
+ * and 16-bit inputs, stage 1 writes dS (into dbias, or into the workspace for
+ * a gradient summed over broadcast dimensions) and stage 2 computes dQ from
+ * it: stage 2 must follow stage 1.  No reference counterpart (the reference
+ * had one fused Triton backward, kernels/backward_kernel.py:17-205). */
 int32_t fa_bwd_stage(const fa_bwd_args* args, void* workspace, size_t workspace_bytes, int32_t stage,
                      void* hip_stream);
 
