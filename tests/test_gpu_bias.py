@@ -347,26 +347,31 @@ def test_bias_long_causal():
 # small cases above do not.  O and LSE of a subset of heads against the
 # oracle and the envelope.
 STAGED = [
-    (torch.bfloat16, 1, 512, 512, 128, 128, 64, True),
-    (torch.float16, 2, 500, 504, 64, 16, 128, False),
-    (torch.bfloat16, 1, 300, 1024, 256, 256, 32, True),
-    (torch.bfloat16, 2, 520, 520, 64, 64, 128, True),
+    # dtype, B, Sq, Sk, H, Hkv, D, causal, bias shape (None: (B, H, Sq, Sk))
+    (torch.bfloat16, 1, 512, 512, 128, 128, 64, True, None),
+    (torch.float16, 2, 500, 504, 64, 16, 128, False, None),
+    (torch.bfloat16, 1, 300, 1024, 256, 256, 32, True, None),
+    (torch.bfloat16, 2, 520, 520, 64, 64, 128, True, None),
+    # broadcast biases (zero batch / head / query strides)
+    (torch.bfloat16, 2, 512, 512, 64, 64, 128, True, (1, 64, 512, 512)),
+    (torch.float16, 2, 512, 520, 64, 32, 64, False, (2, 1, 1, 520)),
 ]
 
 
-@pytest.mark.parametrize("case", STAGED, ids=[f"{c[0]}-B{c[1]}-Sq{c[2]}-Sk{c[3]}-H{c[4]}-D{c[6]}-{c[7]}" for c in STAGED])
+@pytest.mark.parametrize("case", STAGED, ids=[f"{c[0]}-B{c[1]}-Sq{c[2]}-Sk{c[3]}-H{c[4]}-D{c[6]}-{c[7]}-{c[8]}" for c in STAGED])
 def test_bias_staged_forward(case):
-    dt, B, Sq, Sk, H, Hkv, D, causal = case
+    dt, B, Sq, Sk, H, Hkv, D, causal, bshape = case
     say(f"case: staged-bias forward {case}")
     q, k, v, _ = make_inputs(B, Sq, H, D, dt, Sk=Sk, Hkv=Hkv, seed=24)
-    bias = make_bias((B, H, Sq, Sk), dt)
+    bias = make_bias(bshape or (B, H, Sq, Sk), dt)
     scale = D ** -0.5
     o, lse, _ = _lib.fwd(q.to(DEV), k.to(DEV), v.to(DEV), causal, scale, bias=bias.to(DEV))
     torch.cuda.synchronize()
     g = H // Hkv
     for hh in (0, H // 2 + 1, H - 1):
         kh = hh // g
-        qs, ks, vs, bs = q[:, :, hh:hh + 1], k[:, :, kh:kh + 1], v[:, :, kh:kh + 1], bias[:, hh:hh + 1]
+        bh = bias[:, hh:hh + 1] if bias.shape[1] > 1 else bias
+        qs, ks, vs, bs = q[:, :, hh:hh + 1], k[:, :, kh:kh + 1], v[:, :, kh:kh + 1], bh
         ro, rl = oa.attention_forward(qs, ks, vs, causal, scale, None, 0.0, torch.float64, bias=bs)
         eo, el = lowp_math(qs.to(DEV), ks.to(DEV), vs.to(DEV), None, causal, scale, with_bwd=False, bias=bs.to(DEV))
         res = {"O": [maxabs(o[:, :, hh:hh + 1].cpu(), ro), maxabs(eo.cpu(), ro), ro.abs().max().item()],
