@@ -122,9 +122,10 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
     const int tid = threadIdx.x;
     // wave index as a scalar: loop bounds derived from it stay wave-uniform
     const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
-    const int bhk = L / n_ktiles;
-    const int kt = L - bhk * n_ktiles;
+    // key block kt = 0 sees the most queries (causal): rank order is kt order
+    const int2 tord = tile_order<32 * ((std::is_void<TB>::value || D <= 64) && !(Elem<T>::kF32 && D == 128) ? 2 : 1)>(n_ktiles);
+    const int bhk = tord.x;
+    const int kt = tord.y;
     const int hk = bhk % p.Hkv, b = bhk / p.Hkv;
     const int k0 = kt * C::BK;
     const int kw0 = k0 + 32 * w;
@@ -531,9 +532,9 @@ __global__ __launch_bounds__(512, 1) void dkdv8_kernel(const BwdParams p, const 
     const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
     const int kb = w & 3;   // key block
     const int st = w >> 2;  // query sub-step of every tile
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
-    const int bhk = L / n_ktiles;
-    const int kt = L - bhk * n_ktiles;
+    const int2 tord = tile_order<32>(n_ktiles);  // kt = 0 sees the most queries
+    const int bhk = tord.x;
+    const int kt = tord.y;
     const int hk = bhk % p.Hkv, b = bhk / p.Hkv;
     const int k0 = kt * C::BK;
     const int kw0 = k0 + 32 * kb;
@@ -866,9 +867,9 @@ __global__ __launch_bounds__(256 * KS, (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)) 
     const int lane = tid & 63, wg = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
     // w: the wave's 32-query block, sp: its key split (compile-time 0 without one)
     const int w = KS == 1 ? wg : wg & 3, sp = KS == 1 ? 0 : wg >> 2;
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = L / n_qtiles;
-    const int qt = n_qtiles - 1 - (L - bh * n_qtiles);
+    const int2 tord = tile_order<32 * (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)>(n_qtiles);
+    const int bh = tord.x;
+    const int qt = n_qtiles - 1 - tord.y;  // longest causal rows first
     const int h = bh % p.H, b = bh / p.H;
     const int hk = h / p.group;
     const int q0 = qt * C::BM;
@@ -1169,9 +1170,9 @@ __global__ __launch_bounds__(256, 2) void dq_ds_kernel(const BwdParams p, const 
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = L / n_qtiles;
-    const int qt = n_qtiles - 1 - (L - bh * n_qtiles);
+    const int2 tord = tile_order<64>(n_qtiles);
+    const int bh = tord.x;
+    const int qt = n_qtiles - 1 - tord.y;  // longest causal rows first
     const int h = bh % p.H, b = bh / p.H;
     const int hk = h / p.group;
     const int q0 = qt * C::BM;

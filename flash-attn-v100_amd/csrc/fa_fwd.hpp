@@ -86,9 +86,9 @@ __global__ __launch_bounds__(256 * KS * QG, KS == 1 && QG == 1 ? 2 : 1) void fwd
     const int w = KS == 1 && QG == 1 ? wg : wg & 3, sp = KS == 1 ? 0 : wg >> 2;
     const int qg = QG == 1 ? 0 : wg >> 2;
 
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = L / p.n_qtiles;
-    const int qt = p.n_qtiles - 1 - (L - bh * p.n_qtiles);  // longest causal rows first
+    const int2 tord = tile_order<32 * (KS == 1 && QG == 1 ? 2 : 1)>(p.n_qtiles);
+    const int bh = tord.x;
+    const int qt = p.n_qtiles - 1 - tord.y;  // longest causal rows first
     const int h = bh % p.H, b = bh / p.H;
     const int hk = h / p.group;
     const int q0 = qt * C::BM * QG;  // the workgroup's first query
@@ -589,9 +589,9 @@ __global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const FwdParams p) {
     // the two waves of a SIMD own adjacent 32-query blocks (similar causal work)
     const int blk = 2 * (w & 3) + grp;
 
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
-    const int bh = L / p.n_qtiles;
-    const int qt = p.n_qtiles - 1 - (L - bh * p.n_qtiles);  // longest causal rows first
+    const int2 tord = tile_order<32>(p.n_qtiles);
+    const int bh = tord.x;
+    const int qt = p.n_qtiles - 1 - tord.y;  // longest causal rows first
     const int h = bh % p.H, b = bh / p.H;
     const int hk = h / p.group;
     const int q0 = qt * C::BM;
