@@ -120,15 +120,17 @@ def gpu_bench(steps: int, warmup: int, bias_kind: str = "none", want_dbias: bool
         e1.synchronize()
         return e0.elapsed_time(e1) / n  # ms
 
+    # the stages fa_bwd runs (include/fa_abi.h): with dQ read from the stored
+    # dS, the delta pre-pass (0), dK/dV (1), dQ (2); otherwise the dQ pass that
+    # also writes the delta rows (3), then dK/dV (1)
+    stages = (0, 1, 2) if (bias_kind != "none" and want_dbias) else (3, 1)
     n = max(steps, 10)
     fwd_ms = timed(fwd, n)
-    delta_ms = timed(lambda: bwd_stage(0), n)
-    dkdv_ms = timed(lambda: bwd_stage(1), n)
-    dq_ms = timed(lambda: bwd_stage(2), n)
+    stage_ms = {s: timed(lambda s=s: bwd_stage(s), n) for s in stages}
     fwd_bwd_ms = timed(step, n)
     ok = bool(torch.isfinite(o).all() and torch.isfinite(dq).all() and torch.isfinite(dk).all()
               and torch.isfinite(dv).all())
-    return dict(t_step=t_step, fwd_ms=fwd_ms, delta_ms=delta_ms, dkdv_ms=dkdv_ms, dq_ms=dq_ms,
+    return dict(t_step=t_step, fwd_ms=fwd_ms, stage_ms=stage_ms,
                 fwd_bwd_ms=fwd_bwd_ms, finite=ok, device=torch.cuda.get_device_name(0))
 
 
@@ -362,11 +364,16 @@ def main():
     Ftot = 3.5 * F
     value = Ftot / r["t_step"] / 1e12
     fwd_tflops = F / (r["fwd_ms"] * 1e-3) / 1e12
-    kernels = {"fwd_kernel": r["fwd_ms"], "delta_kernel": r["delta_ms"], "dkdv_kernel": r["dkdv_ms"],
-               "dq_kernel": r["dq_ms"]}
+    names = {0: "delta_kernel", 1: "dkdv_kernel", 2: "dq_kernel", 3: "dq_kernel"}
+    kernels = {"fwd_kernel": r["fwd_ms"]}
+    kernels.update({names[st]: ms for st, ms in r["stage_ms"].items()})
     # the kernels each stage launches at this workload (the keys above name the stages)
-    stage_kernels = {"fwd_kernel": "fwd_kernel (128-query workgroups)", "delta_kernel": "delta_kernel",
-                     "dkdv_kernel": "dkdv_kernel", "dq_kernel": "dq_kernel"}
+    stage_kernels = {"fwd_kernel": "fwd_kernel (128-query workgroups)", "dkdv_kernel": "dkdv_kernel"}
+    if 3 in r["stage_ms"]:
+        stage_kernels["dq_kernel"] = "dq_kernel (computes and writes the delta rows; runs before dK/dV)"
+    else:
+        stage_kernels["delta_kernel"] = "delta_kernel"
+        stage_kernels["dq_kernel"] = "dq_kernel"
     if a.bias != "none":
         stage_kernels["fwd_kernel"] = "fwd_kernel (256-query workgroups, bias staged through LDS)"
         stage_kernels["dkdv_kernel"] = "dkdv8_kernel" + (" + dbias_reduce_kernel" if a.bias == "heads" and a.dbias else "")

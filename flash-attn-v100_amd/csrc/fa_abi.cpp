@@ -390,7 +390,7 @@ int32_t fa_bwd_check(const fa_bwd_args* a, size_t ws_bytes) {
 }
 
 int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int32_t stage, void* stream) {
-    if (stage < -1 || stage > 2) return FA_ERR_SHAPE;
+    if (stage < -1 || stage > 3) return FA_ERR_SHAPE;
     int32_t st = fa_bwd_check(a, ws_bytes);
     if (st) return st;
     const size_t need = fa_bwd_workspace_size(a);
@@ -497,6 +497,9 @@ int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int
             }
         }
     }
+    // stage 3 is the dQ pass that recomputes dS; one that reads the dK/dV
+    // pass's dS cannot run before it
+    if (stage == 3 && p.dq_from_ds) return FA_ERR_SHAPE;
     const bool causal = a->causal != 0;
     const bool dropout = a->dropout_p > 0.f;
     hipStream_t s = (hipStream_t)stream;

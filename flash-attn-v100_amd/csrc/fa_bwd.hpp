@@ -859,6 +859,7 @@ __global__ __launch_bounds__(256 * KS, (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)) 
     using C = DqCfg<T, D>;
     constexpr bool BIAS = !std::is_void<TB>::value;
     using BT = typename std::conditional<BIAS, TB, T>::type;
+    using BT16 = typename std::conditional<C::F32, bf16, T>::type;  // the 16-bit input type
     constexpr int BN = C::BN, KW = C::KW;
     __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES * KS];
 
@@ -877,10 +878,12 @@ __global__ __launch_bounds__(256 * KS, (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)) 
     const int qi = qw0 + l32;
 
     constexpr int QR = C::F32 ? D / 8 : D / 16;
-    uint4 qreg[QR], doreg[QR];
+    const bool own_delta = !C::F32 && p.dq_delta;
+    uint4 qreg[QR], doreg[QR], oreg[C::F32 ? 1 : QR];
     {
         const T* qrow = (const T*)p.q + b * p.q_sb + (int64_t)qi * p.q_ss + h * p.q_sh;
         const T* drow = (const T*)p.dout + b * p.do_sb + (int64_t)qi * p.do_ss + h * p.do_sh;
+        const T* orow = (const T*)p.o + b * p.o_sb + (int64_t)qi * p.o_ss + h * p.o_sh;
 #pragma unroll
         for (int i = 0; i < QR; ++i) {
             const int d0 = C::F32 ? hi * (D / 2) + 4 * i : 16 * i + 8 * hi;
@@ -888,10 +891,23 @@ __global__ __launch_bounds__(256 * KS, (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)) 
             qreg[i] = ok ? *reinterpret_cast<const uint4*>(qrow + d0) : make_uint4(0u, 0u, 0u, 0u);
             doreg[i] = ok ? *reinterpret_cast<const uint4*>(drow + d0) : make_uint4(0u, 0u, 0u, 0u);
         }
+        if constexpr (!C::F32) {
+            if (own_delta) {
+#pragma unroll
+                for (int i = 0; i < QR; ++i)
+                    oreg[i] = qi < p.Sq ? *reinterpret_cast<const uint4*>(orow + 16 * i + 8 * hi)
+                                        : make_uint4(0u, 0u, 0u, 0u);
+            }
+        }
     }
     const int64_t wi = ((int64_t)b * p.H + h) * p.ws_stride + qi;  // qi < sq_pad
-    const float lse2 = p.lse2[wi];
-    const float del = p.delta[wi];
+    float lse2 = 0.f, del = 0.f, lse_in = 0.f;
+    if (own_delta)
+        lse_in = qi < p.Sq ? p.lse[((int64_t)b * p.H + h) * p.Sq + qi] : -INFINITY;
+    else {
+        lse2 = p.lse2[wi];
+        del = p.delta[wi];
+    }
     // no wait here: these loads stay in flight while the first tile copy is
     // issued (the loop's first barrier waits for both)
     const float c = p.scale_log2;
@@ -941,6 +957,36 @@ __global__ __launch_bounds__(256 * KS, (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)) 
     // (never read), so the copy is branch-free.
     int bcur = 0;
     if (n_tl > 0) issue(0, 0);
+
+    if constexpr (!C::F32) {
+        if (own_delta) {
+            // no pre-pass: delta = rowsum(dO * O) of this lane's query from its
+            // half of the row (16-byte chunks 2 i + hi) plus the other half in
+            // lane l ^ 32, summed in the order delta_kernel sums the row's
+            // chunks (chunk sums, then a pairwise tree), so both give the same
+            // bits; the rows go to the workspace for the dK/dV pass, which runs
+            // after this one.  Rows past Sq: delta = 0, LSE * log2 e = +inf.
+            float cs[QR];
+#pragma unroll
+            for (int i = 0; i < QR; ++i) {
+                const s16x8 a = __builtin_bit_cast(s16x8, oreg[i]), d = __builtin_bit_cast(s16x8, doreg[i]);
+                float acc = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc += Elem<BT16>::unpack1(a[e]) * Elem<BT16>::unpack1(d[e]);
+                cs[i] = acc;
+            }
+#pragma unroll
+            for (int st = QR / 2; st > 0; st >>= 1)
+#pragma unroll
+                for (int i = 0; i < st; ++i) cs[i] = cs[i] + cs[i + st];
+            del = pair_sum(cs[0]);
+            lse2 = lse_in == -INFINITY ? INFINITY : lse_in * kLog2e;
+            if (sp == 0 && hi == 0) {
+                p.lse2[wi] = lse2;
+                p.delta[wi] = del;
+            }
+        }
+    }
 
     // bias of this lane's query row (rows past Sq read zeros, keys past Sk read
     // zeros or the next row: both masked)
@@ -1338,7 +1384,26 @@ inline bool dkdv8_runs(const BwdParams& p) {
 }
 
 template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
-hipError_t launch_bwd_t(const BwdParams& p, int stage, hipStream_t s) {
+hipError_t launch_bwd_t(const BwdParams& p0, int stage, hipStream_t s) {
+    // stage 3: the workspace rows and dQ, for a dQ pass that recomputes dS.
+    // 16-bit inputs do both in the dQ kernel (no delta pre-pass); fp32 runs
+    // the pre-pass, then the dQ pass.  The whole backward without a dS pass
+    // is stage 3, then dK/dV.
+    const bool ds_pass = !std::is_void<TB>::value && !Elem<T>::kF32 && p0.dq_from_ds;
+    if (stage == 3 || (stage < 0 && !ds_pass)) {
+        hipError_t e;
+        if constexpr (Elem<T>::kF32) {
+            e = launch_bwd_t<T, D, CAUSAL, DROPOUT, TB>(p0, 0, s);
+            if (e == hipSuccess) e = launch_bwd_t<T, D, CAUSAL, DROPOUT, TB>(p0, 2, s);
+        } else {
+            BwdParams pf = p0;
+            pf.dq_delta = 1;
+            e = launch_bwd_t<T, D, CAUSAL, DROPOUT, TB>(pf, 2, s);
+        }
+        if (e != hipSuccess || stage == 3) return e;
+        return launch_bwd_t<T, D, CAUSAL, DROPOUT, TB>(p0, 1, s);
+    }
+    const BwdParams& p = p0;
     if (stage < 0 || stage == 0) {
         constexpr int EPC = 16 / sizeof(T);
         constexpr int RPB = 256 / (D / EPC);

@@ -87,6 +87,10 @@ struct BwdParams {
     // aligned and Sk * dbias_es is a multiple of 16
     int dq_from_ds;
     int ds_span;  // readable bytes of one (batch, head) dS slice (dq_from_ds)
+    // 1 (set by the launcher, 16-bit inputs): the dQ pass runs first and
+    // computes LSE * log2 e and delta of its query rows itself, writing the
+    // workspace rows the dK/dV pass then reads (no delta pre-pass)
+    int dq_delta;
 };
 
 // Sum of per-(batch, head) dBias slices over broadcast dimensions:
@@ -123,7 +127,9 @@ hipError_t launch_fwd_bias_f16(const FwdParams& p, int D, bool causal, bool drop
 hipError_t launch_fwd_bias_f32(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
 hipError_t launch_fwd_bias32_bf16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
 hipError_t launch_fwd_bias32_f16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
-// stage: 0 = delta pre-pass, 1 = dK/dV, 2 = dQ, -1 = all three in order
+// stage: 0 = delta pre-pass, 1 = dK/dV, 2 = dQ, 3 = the workspace rows and dQ
+// (a recomputing dQ pass), -1 = the whole backward (3 then 1, or 0, 1, 2 when
+// dQ reads the dS of the dK/dV pass)
 hipError_t launch_bwd_bf16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
 hipError_t launch_bwd_f16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
 hipError_t launch_bwd_f32(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);

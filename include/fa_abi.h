@@ -196,13 +196,17 @@ int32_t fa_bwd_check(const fa_bwd_args* args, size_t workspace_bytes);
 int32_t fa_bwd(const fa_bwd_args* args, void* workspace, size_t workspace_bytes, void* hip_stream);
 
 /* One stage of fa_bwd: 0 = delta pre-pass (writes the workspace), 1 = dK/dV,
- * 2 = dQ; -1 = all three (same as fa_bwd).  Without a bias gradient, stages 1
- * and 2 only read the workspace and are independent of each other, so after
- * stage 0 a caller may run them on two streams.  With one (dbias non-NULL)
- * and 16-bit inputs, stage 1 writes dS (into dbias, or into the workspace for
- * a gradient summed over broadcast dimensions) and stage 2 computes dQ from
- * it: stage 2 must follow stage 1.  No reference counterpart (the reference
- * had one fused Triton backward, kernels/backward_kernel.py:17-205). */
+ * 2 = dQ, 3 = the workspace rows and dQ in one pass (16-bit inputs: the dQ
+ * kernel computes delta itself; fp32: stage 0 then stage 2); -1 = the whole
+ * backward (same as fa_bwd: stage 3 then stage 1, or 0, 1, 2 when dQ reads
+ * dS, below).  Without a bias gradient, stages 1 and 2 only read the
+ * workspace and are independent of each other, so after stage 0 a caller may
+ * run them on two streams; stage 1 after stage 3 gives the same results.
+ * With one (dbias non-NULL) and 16-bit inputs, stage 1 writes dS (into dbias,
+ * or into the workspace for a gradient summed over broadcast dimensions) and
+ * stage 2 computes dQ from it: stage 2 must follow stage 1, and stage 3 is
+ * FA_ERR_SHAPE.  No reference counterpart (the reference had one fused Triton
+ * backward, kernels/backward_kernel.py:17-205). */
 int32_t fa_bwd_stage(const fa_bwd_args* args, void* workspace, size_t workspace_bytes, int32_t stage,
                      void* hip_stream);
 
@@ -214,7 +218,7 @@ int32_t fa_bwd_stage(const fa_bwd_args* args, void* workspace, size_t workspace_
  * Every call on one GPU shares that GPU's scratch: calls that overlap on one
  * GPU (on different streams, or from different threads) race, so a caller
  * serialises them (one stream, or its own ordering).  No scratch contents carry
- * over between calls: stage 0 writes every workspace row the later stages read.
+ * over between calls: stage 0 (or 3) writes every workspace row the later stages read.
  * The first call on a GPU looks the array's device address up once
  * (hipGetSymbolAddress).
  * No counterpart in the reference: for callers that cannot allocate device

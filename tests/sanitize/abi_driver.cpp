@@ -206,13 +206,13 @@ static void bwd_paths() {
     CHECK(fa_bwd_check(&a, ws) == FA_OK);
     CHECK(fa_bwd_check(&a, ws - 4) == FA_ERR_WORKSPACE);
     CHECK(fa_bwd(&a, nullptr, ws, nullptr) == FA_ERR_WORKSPACE);
-    CHECK(fa_bwd_stage(&a, w, ws, 3, nullptr) == FA_ERR_SHAPE);
+    CHECK(fa_bwd_stage(&a, w, ws, 4, nullptr) == FA_ERR_SHAPE);
     CHECK(fa_bwd_stage(&a, w, ws, -2, nullptr) == FA_ERR_SHAPE);
     CHECK(fa_bwd(&a, w, ws, nullptr) == FA_OK);
     CHECK(std::strcmp(g_stub.last, "launch_bwd_bf16") == 0 && g_stub.stage == -1);
     CHECK(g_stub.bwd.sq_pad == 128 && g_stub.bwd.ws_stride == 256 && g_stub.bwd.group == 2);
     CHECK(g_stub.bwd.lse2 == (float*)w && g_stub.bwd.delta == (float*)w + 128);
-    for (int s = 0; s < 3; ++s) {
+    for (int s = 0; s < 4; ++s) {
         CHECK(fa_bwd_stage(&a, w, ws, s, nullptr) == FA_OK);
         CHECK(g_stub.stage == s);
     }
@@ -231,6 +231,8 @@ static void bwd_paths() {
     const size_t rows = (size_t)(3 * 4 * 2 * 128 * 4 + 255) / 256 * 256;
     CHECK(wsb == rows + (size_t)(3 * 4 * 70 * 72 * 4 + 255) / 256 * 256);
     const int r0 = g_stub.reduce_calls;
+    // dQ reads the stored dS here: it cannot run as the first pass (stage 3)
+    CHECK(fa_bwd_stage(&b, alloc(wsb), wsb, 3, nullptr) == FA_ERR_SHAPE);
     CHECK(fa_bwd(&b, alloc(wsb), wsb, nullptr) == FA_OK);
     CHECK(g_stub.reduce_calls == r0 + 1 && g_stub.reduce.sum_b == 1 && g_stub.reduce.sum_h == 0);
     CHECK(g_stub.reduce.SkP == 72 && g_stub.bwd.dbias_dtype == FA_DTYPE_F32 && g_stub.bwd.dbias_zero_fill == 0);

@@ -225,7 +225,8 @@ def test_bwd_workspace_and_checks():
     assert ws == ((B * H * 2 * sq_pad * 4 + 255) // 256) * 256
     assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_OK"]
     assert lib.fa_bwd_check(ctypes.byref(a), ws - 4) == CODES["FA_ERR_WORKSPACE"]
-    assert lib.fa_bwd_stage(ctypes.byref(a), None, ws, 3, None) == CODES["FA_ERR_SHAPE"]
+    assert lib.fa_bwd_stage(ctypes.byref(a), None, ws, 4, None) == CODES["FA_ERR_SHAPE"]
+    assert lib.fa_bwd_stage(ctypes.byref(a), None, ws, -2, None) == CODES["FA_ERR_SHAPE"]
     assert lib.fa_bwd(ctypes.byref(a), None, ws, None) == CODES["FA_ERR_WORKSPACE"]
     a.dq = None
     assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_ERR_NULL_ARG"]

@@ -225,6 +225,36 @@ def test_empty_keys():
     assert torch.equal(o, torch.zeros_like(o)) and bool((lse == float("-inf")).all())
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_bwd_stage3_equals_prepass_then_dq(dt, D):
+    # include/fa_abi.h: stage 3 writes the workspace rows and dQ in one pass
+    # (16-bit: the dQ kernel computes delta itself, summing as the pre-pass
+    # does); its rows and dQ equal stage 0 then stage 2 bit for bit, including
+    # the padding rows past Sq and rows whose LSE is -inf
+    import ctypes
+    say(f"case: stage 3 vs stages 0 + 2, {dt} D={D}")
+    B, S, H = 2, 300, 4
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, S, H, D, dt, Hkv=2, seed=37))
+    o, lse, _ = _lib.fwd(q, k, v, True, D ** -0.5)
+    lse[0, 1, 5] = float("-inf")
+    lib = _lib.load()
+    outs = []
+    for stages in ((0, 2), (3,)):
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        a = _lib.bwd_args(q, k, v, o, do, lse, dq, dk, dv, True, D ** -0.5, 0.0, 0, 0)
+        nbytes = lib.fa_bwd_workspace_size(ctypes.byref(a))
+        ws = torch.full((nbytes // 4,), 7.0, device=DEV)
+        sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for st in stages:
+            assert lib.fa_bwd_stage(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), nbytes, st, sp) == 0
+        torch.cuda.synchronize()
+        rows = B * H * 2 * ((S + 127) // 128 * 128)
+        outs.append((ws[:rows].clone(), dq.clone()))
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1])
+
+
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_bwd_stages_on_two_streams(with_bias):
     # include/fa_abi.h: after stage 0, stages 1 (dK/dV [+ dBias]) and 2 (dQ) are
