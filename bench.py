@@ -368,7 +368,7 @@ def main():
     kernels = {"fwd_kernel": r["fwd_ms"]}
     kernels.update({names[st]: ms for st, ms in r["stage_ms"].items()})
     # the kernels each stage launches at this workload (the keys above name the stages)
-    stage_kernels = {"fwd_kernel": "fwd_kernel (128-query workgroups)", "dkdv_kernel": "dkdv_kernel"}
+    stage_kernels = {"fwd_kernel": "fwd_pp_kernel (256-query ping-pong workgroups)", "dkdv_kernel": "dkdv_kernel"}
     if 3 in r["stage_ms"]:
         stage_kernels["dq_kernel"] = "dq_kernel (computes and writes the delta rows; runs before dK/dV)"
     else:

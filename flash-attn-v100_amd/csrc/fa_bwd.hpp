@@ -1359,9 +1359,12 @@ __global__ __launch_bounds__(256, 2) void dq_ds_kernel(const BwdParams p, const 
         if (kz < p.Sk) {
             const int cpr = (p.Sk - kz) * ES / 16;  // 16-byte chunks per row tail
             char* zb = (char*)p.dbias + (b * p.dbias_sb + h * p.dbias_sh + (int64_t)q0 * p.dbias_ss + kz) * ES;
+            // non-temporal: nothing reads these lines back (C3 with a bias
+            // gradient: 0.98 -> 0.94 ms for this pass)
             for (int r = w; r < nrow; r += C::NW)
                 for (int c = lane; c < cpr; c += 64)
-                    *reinterpret_cast<uint4*>(zb + (int64_t)r * p.dbias_ss * ES + 16 * c) = make_uint4(0u, 0u, 0u, 0u);
+                    __builtin_nontemporal_store(u32x4{0u, 0u, 0u, 0u},
+                                                reinterpret_cast<u32x4*>(zb + (int64_t)r * p.dbias_ss * ES + 16 * c));
         }
     }
 }
