@@ -1095,13 +1095,73 @@ __global__ __launch_bounds__(256 * KS, (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)) 
             }
         }
     };
+    // 16-bit inputs without bias or dropout: the S / dP products of a tile's
+    // two sub-steps are issued before the dS of either, so the dS arithmetic of
+    // the first overlaps the products of the second inside the wave (the same
+    // arithmetic in the same order as `sub`, so the same bits)
+    constexpr bool PIPE = !C::F32 && !BIAS && DROPOUT == 0;
+    using TP = BT16;  // T for the 16-bit inputs these two serve
+    auto sdp16 = [&](const T* Ks, const T* Vs, f32x16& s, f32x16& dp) FA_INLINE {
+        s = f32x16{};
+        dp = f32x16{};
+        const T* krow = Ks + l32 * KW;
+        const T* vrow = Vs + l32 * KW;
+#pragma unroll
+        for (int kk = 0; kk < QR; ++kk) {
+            const s16x8 ak = *reinterpret_cast<const s16x8*>(krow + 16 * kk + 8 * hi);
+            const s16x8 av = *reinterpret_cast<const s16x8*>(vrow + 16 * kk + 8 * hi);
+            s = Elem<TP>::mfma(ak, __builtin_bit_cast(s16x8, qreg[kk]), s);
+            dp = Elem<TP>::mfma(av, __builtin_bit_cast(s16x8, doreg[kk]), dp);
+        }
+    };
+    auto fin16 = [&](int k0, const T* Ks, f32x16& s, const f32x16& dp, auto mask_tag) FA_INLINE {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const bool need_mask = MASK && ((k0 + 32 > p.Sk) || (CAUSAL && k0 + 31 > qw0));
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = k0 + 8 * (r >> 2) + 4 * hi + (r & 3);
+            float pv = fast_exp2(__builtin_fmaf(s[r], c, -lse2));
+            if (need_mask && (key >= p.Sk || (CAUSAL && key > qi))) pv = 0.f;
+            s[r] = pv * (dp[r] - del);
+        }
+        const int trow = 4 * hi + ((lane & 15) >> 2);
+        const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            float ts[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ts[e] = s[8 * ks + e];
+            const s16x8 bs8 = pack8<TP>(ts);
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i) {
+                const T* kp = Ks + (16 * ks + trow) * KW + 32 * i + tcol;
+                const s16x8 a = cat4(lds_read_tr16(kp), lds_read_tr16(kp + 8 * KW));
+                dq[i] = Elem<TP>::mfma(a, bs8, dq[i]);
+            }
+        }
+    };
     auto step = [&](int j, auto mask_tag) FA_INLINE {
         sync_tiles();
         issue(min(j + 1, n_tl - 1), bcur ^ 1);
+        if constexpr (PIPE) {
+            static_assert(C::NSUB == 2, "two sub-steps per tile");
+            constexpr bool MASK = decltype(mask_tag)::value;
+            const int ka = (j * KS + sp) * C::BN, kb2 = ka + 32;
+            const T* ksa = (const T*)buf(bcur);
+            const T* vsa = (const T*)(buf(bcur) + C::KALLOC);
+            const bool act_a = !MASK || !CAUSAL || ka <= qw0 + 31;
+            const bool act_b = !MASK || !CAUSAL || kb2 <= qw0 + 31;
+            f32x16 sa, dpa, sb, dpb;
+            if (act_a) sdp16(ksa, vsa, sa, dpa);
+            if (act_b) sdp16(ksa + 32 * KW, vsa + 32 * KW, sb, dpb);
+            if (act_a) fin16(ka, ksa, sa, dpa, mask_tag);
+            if (act_b) fin16(kb2, ksa + 32 * KW, sb, dpb, mask_tag);
+        } else {
 #pragma unroll
-        for (int st = 0; st < C::NSUB; ++st)
-            sub((j * KS + sp) * C::BN + 32 * st, (const T*)buf(bcur) + 32 * st * KW,
-                (const T*)(buf(bcur) + C::KALLOC) + 32 * st * KW, mask_tag);
+            for (int st = 0; st < C::NSUB; ++st)
+                sub((j * KS + sp) * C::BN + 32 * st, (const T*)buf(bcur) + 32 * st * KW,
+                    (const T*)(buf(bcur) + C::KALLOC) + 32 * st * KW, mask_tag);
+        }
         bcur ^= 1;
     };
 

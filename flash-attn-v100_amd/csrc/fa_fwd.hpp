@@ -669,7 +669,7 @@ __global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const FwdParams p) {
     constexpr int NPV = (BN / 16) * (D / 32);  // PV MFMAs per tile
     static_assert(NQK == NPV, "one S and one PV product per step");
     constexpr int NSTEP = NQK;
-    constexpr int MP = 3;
+    constexpr int MP = 2;  // measured against 1, 3, 4, 5 (3: 1-2% slower, 1: 7%)
     auto kfrag = [&](const T* Ks, int t) FA_INLINE {
         const int bk = t / QR, kk = t % QR;
         return *reinterpret_cast<const s16x8*>(Ks + (32 * bk + l32) * KW + 16 * kk + 8 * hi);
