@@ -26,9 +26,15 @@ ARCH = "gfx950"
 SOURCES = ["fa_abi.cpp", "fa_misc.hip"] + [
     f"fa_{pas}_{mode}{dt}.hip"
     for pas in ("bwd", "fwd")  # the backward units take longest: start them first
-    for mode, dts in (("", ("bf16", "f16", "f32")), ("bias_", ("bf16", "f16", "f32")), ("bias32_", ("bf16", "f16")))
+    for mode, dts in (("d256_", ("bf16", "f16")), ("", ("bf16", "f16", "f32")), ("bias_", ("bf16", "f16", "f32")),
+                      ("bias32_", ("bf16", "f16")))
     for dt in dts
 ]
+
+# units whose MFMA accumulators may live in AGPRs (the head-dim-256 backward:
+# its dK / dV and dQ kernels need more than 256 registers a lane; with the
+# accumulators forced into VGPR form the compiler crashes on them)
+AGPR_FORM_SOURCES = ("fa_bwd_d256_bf16.hip", "fa_bwd_d256_f16.hip")
 
 
 def hipcc() -> str:
@@ -63,9 +69,17 @@ def common_flags():
     ]
 
 
+def flags_for(src: str):
+    f = common_flags()
+    if src in AGPR_FORM_SOURCES:
+        i = f.index("-amdgpu-mfma-vgpr-form=true")
+        del f[i - 1:i + 1]
+    return f
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc()] + common_flags() + ["-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc()] + flags_for(src) + ["-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {src}\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -104,7 +104,8 @@ int32_t check_common(int32_t B, int32_t Sq, int32_t Sk, int32_t H, int32_t Hkv, 
                      float scale, float dropout_p) {
     if (B < 0 || Sq < 0 || Sk < 0 || H < 0 || Hkv < 0) return FA_ERR_SHAPE;
     if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F32) return FA_ERR_DTYPE;
-    if (D != 32 && D != 64 && D != 128) return FA_ERR_HEAD_DIM;
+    // 256: 16-bit inputs only (and no bias: fa_fwd_check / fa_bwd_check)
+    if (D != 32 && D != 64 && D != 128 && !(D == 256 && dtype != FA_DTYPE_F32)) return FA_ERR_HEAD_DIM;
     if (H == 0 || Hkv == 0 || H % Hkv != 0) return FA_ERR_HEADS;
     if (!std::isfinite(scale) || !(scale > 0.f)) return FA_ERR_SCALE;
     if (!std::isfinite(dropout_p) || dropout_p < 0.f || dropout_p >= 1.f) return FA_ERR_DROPOUT;
@@ -241,7 +242,7 @@ const char* fa_strerror(int32_t code) {
         case FA_OK: return "success";
         case FA_ERR_NULL_ARG: return "a required pointer is NULL";
         case FA_ERR_SHAPE: return "a size is negative or inconsistent";
-        case FA_ERR_HEAD_DIM: return "head_dim must be 32, 64 or 128";
+        case FA_ERR_HEAD_DIM: return "head_dim must be 32, 64 or 128 (or 256 for fp16 / bf16 inputs without a bias)";
         case FA_ERR_DTYPE: return "dtype must be FA_DTYPE_F16, FA_DTYPE_BF16 or FA_DTYPE_F32";
         case FA_ERR_STRIDE: return "the d stride must be 1 and the b/s/h strides multiples of 16 bytes";
         case FA_ERR_HEADS: return "num_heads must be a positive multiple of num_heads_kv";
@@ -283,6 +284,7 @@ int32_t fa_fwd_check(const fa_fwd_args* a) {
         (st = check_span(a->o_stride, a->seqlen_q, a->head_dim, es)))
         return st;
     if ((uintptr_t)a->keep_bits & 3u) return FA_ERR_ALIGN;
+    if (a->bias && a->head_dim == 256) return FA_ERR_HEAD_DIM;
     return check_bias(a->bias, a->bias_stride, a->bias_dtype, a->dtype, a->seqlen_q, a->seqlen_k);
 }
 
@@ -341,9 +343,14 @@ int32_t fa_fwd(const fa_fwd_args* a, void* stream) {
             default: return status_of(fa::launch_fwd_bias_f32(p, a->head_dim, causal, dropout, s));
         }
     }
+    const bool d256 = a->head_dim == 256;
     switch (a->dtype) {
-        case FA_DTYPE_BF16: return status_of(fa::launch_fwd_bf16(p, a->head_dim, causal, dropout, s));
-        case FA_DTYPE_F16: return status_of(fa::launch_fwd_f16(p, a->head_dim, causal, dropout, s));
+        case FA_DTYPE_BF16:
+            return status_of(d256 ? fa::launch_fwd_d256_bf16(p, a->head_dim, causal, dropout, s)
+                                  : fa::launch_fwd_bf16(p, a->head_dim, causal, dropout, s));
+        case FA_DTYPE_F16:
+            return status_of(d256 ? fa::launch_fwd_d256_f16(p, a->head_dim, causal, dropout, s)
+                                  : fa::launch_fwd_f16(p, a->head_dim, causal, dropout, s));
         default: return status_of(fa::launch_fwd_f32(p, a->head_dim, causal, dropout, s));
     }
 }
@@ -380,6 +387,7 @@ int32_t fa_bwd_check(const fa_bwd_args* a, size_t ws_bytes) {
     for (int i = 0; i < 8; ++i)
         if ((st = check_span(strides[i], rows[i], a->head_dim, es))) return st;
     if (a->dbias && !a->bias) return FA_ERR_BIAS;
+    if (a->bias && a->head_dim == 256) return FA_ERR_HEAD_DIM;
     if ((uintptr_t)a->keep_bits & 3u) return FA_ERR_ALIGN;
     if ((st = check_bias(a->bias, a->bias_stride, a->bias_dtype, a->dtype, a->seqlen_q, a->seqlen_k)) ||
         (st = check_dbias(a)))
@@ -522,9 +530,14 @@ int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int
         if (e == hipSuccess && reduce_db && (stage < 0 || stage == 1)) e = fa::launch_dbias_reduce(rp, s);
         return status_of(e);
     }
+    const bool d256 = a->head_dim == 256;
     switch (a->dtype) {
-        case FA_DTYPE_BF16: return status_of(fa::launch_bwd_bf16(p, a->head_dim, causal, dropout, stage, s));
-        case FA_DTYPE_F16: return status_of(fa::launch_bwd_f16(p, a->head_dim, causal, dropout, stage, s));
+        case FA_DTYPE_BF16:
+            return status_of(d256 ? fa::launch_bwd_d256_bf16(p, a->head_dim, causal, dropout, stage, s)
+                                  : fa::launch_bwd_bf16(p, a->head_dim, causal, dropout, stage, s));
+        case FA_DTYPE_F16:
+            return status_of(d256 ? fa::launch_bwd_d256_f16(p, a->head_dim, causal, dropout, stage, s)
+                                  : fa::launch_bwd_f16(p, a->head_dim, causal, dropout, stage, s));
         default: return status_of(fa::launch_bwd_f32(p, a->head_dim, causal, dropout, stage, s));
     }
 }

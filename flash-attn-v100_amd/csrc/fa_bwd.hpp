@@ -111,7 +111,7 @@ struct DkdvCfg {
 
 // TB: element type of the additive bias (T or float), void = no bias
 template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
-__global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Elem<T>::kF32 && D == 128) ? 2 : 1)) void dkdv_kernel(
+__global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Elem<T>::kF32 && D == 128) && D <= 128 ? 2 : 1)) void dkdv_kernel(
     const BwdParams p, const int n_ktiles) {
     using C = DkdvCfg<T, D>;
     constexpr bool BIAS = !std::is_void<TB>::value;
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
     // wave index as a scalar: loop bounds derived from it stay wave-uniform
     const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
     // key block kt = 0 sees the most queries (causal): rank order is kt order
-    const int2 tord = tile_order<32 * ((std::is_void<TB>::value || D <= 64) && !(Elem<T>::kF32 && D == 128) ? 2 : 1)>(n_ktiles);
+    const int2 tord = tile_order<32 * ((std::is_void<TB>::value || D <= 64) && !(Elem<T>::kF32 && D == 128) && D <= 128 ? 2 : 1)>(n_ktiles);
     const int bhk = tord.x;
     const int kt = tord.y;
     const int hk = bhk % p.Hkv, b = bhk / p.Hkv;
@@ -847,7 +847,7 @@ struct DqCfg {
     static constexpr int STAGE_BYTES = NW * 32 * OW * (int)sizeof(T);
     static constexpr int SMEM_BYTES = NBUF * BUF_BYTES > STAGE_BYTES ? NBUF * BUF_BYTES : STAGE_BYTES;
     // fp32 at D=128 needs more than 256 registers per lane (Q, dO and dQ^T in fp32)
-    static constexpr int MIN_BLOCKS = (F32 && D == 128) ? 1 : 2;
+    static constexpr int MIN_BLOCKS = ((F32 && D == 128) || D > 128) ? 1 : 2;
 };
 
 // KS: key split, as in fwd_kernel: KS groups of 4 waves on the same 128
@@ -1437,7 +1437,7 @@ __global__ __launch_bounds__(256, 2) void dq_ds_kernel(const BwdParams p, const 
 // the causal dBias is needed (rows not 16-byte aligned).
 template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
 inline bool dkdv8_runs(const BwdParams& p) {
-    if constexpr (!Elem<T>::kF32 && DROPOUT == 0 && D >= 64) {
+    if constexpr (!Elem<T>::kF32 && DROPOUT == 0 && D >= 64 && D <= 128) {
         constexpr bool BIAS = !std::is_void<TB>::value;
         const int64_t nb = (int64_t)((p.Sk + DkdvCfg<T, D>::BK - 1) / DkdvCfg<T, D>::BK) * p.Hkv * p.B;
         const bool fill1 = BIAS && CAUSAL && p.dbias != nullptr && p.dbias_zero_fill == 1;
@@ -1479,7 +1479,7 @@ hipError_t launch_bwd_t(const BwdParams& p0, int stage, hipStream_t s) {
         const int nk = (p.Sk + C::BK - 1) / C::BK;
         const int64_t nb = (int64_t)nk * p.Hkv * p.B;
         bool done = false;
-        if constexpr (!Elem<T>::kF32 && DROPOUT == 0 && D >= 64) {
+        if constexpr (!Elem<T>::kF32 && DROPOUT == 0 && D >= 64 && D <= 128) {
             static_assert(Dkdv8Cfg<T, D>::BK == C::BK, "same key blocks");
             if (dkdv8_runs<T, D, CAUSAL, DROPOUT, TB>(p)) {
                 hipLaunchKernelGGL((dkdv8_kernel<T, D, CAUSAL, TB>), dim3((unsigned)nb), dim3(Dkdv8Cfg<T, D>::NT), 0, s, p,
@@ -1545,6 +1545,23 @@ hipError_t launch_bwd_dispatch(const BwdParams& p, int D, bool causal, bool drop
 #undef FA_BWD_CASE
 #undef FA_BWD_MODES
     return hipErrorInvalidValue;
+}
+
+// Head dim 256 (16-bit inputs, no bias): one workgroup per CU for dK/dV and
+// dQ (translation units of their own, fa_bwd_d256_*.hip).
+template <typename T>
+hipError_t launch_bwd_d256(const BwdParams& p, bool causal, bool dropout, int stage, hipStream_t s) {
+    static_assert(!Elem<T>::kF32, "16-bit inputs");
+    const int mode = !dropout ? 0 : (p.kb != nullptr ? 2 : 1);
+#define FA_BWD_MODES(CC)                                                    \
+    switch (mode) {                                                         \
+        case 0: return launch_bwd_t<T, 256, CC, 0, void>(p, stage, s);      \
+        case 1: return launch_bwd_t<T, 256, CC, 1, void>(p, stage, s);      \
+        default: return launch_bwd_t<T, 256, CC, 2, void>(p, stage, s);     \
+    }
+    if (causal) FA_BWD_MODES(true)
+    FA_BWD_MODES(false)
+#undef FA_BWD_MODES
 }
 
 }  // namespace fa

@@ -66,7 +66,7 @@ struct FwdCfg {
 // per lane) touch 32 rows per instruction.  The LDS of one such workgroup
 // holds the K/V tiles and the 8 bias regions.
 template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB, int KS, int QG = 1>
-__global__ __launch_bounds__(256 * KS * QG, KS == 1 && QG == 1 ? 2 : 1) void fwd_kernel(const FwdParams p) {
+__global__ __launch_bounds__(256 * KS * QG, KS == 1 && QG == 1 && D <= 128 ? 2 : 1) void fwd_kernel(const FwdParams p) {
     using C = FwdCfg<T, D>;
     constexpr bool BIAS = !std::is_void<TB>::value;
     using BT = typename std::conditional<BIAS, TB, T>::type;
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256 * KS * QG, KS == 1 && QG == 1 ? 2 : 1) void fwd
     const int w = KS == 1 && QG == 1 ? wg : wg & 3, sp = KS == 1 ? 0 : wg >> 2;
     const int qg = QG == 1 ? 0 : wg >> 2;
 
-    const int2 tord = tile_order<32 * (KS == 1 && QG == 1 ? 2 : 1)>(p.n_qtiles);
+    const int2 tord = tile_order<32 * (KS == 1 && QG == 1 && D <= 128 ? 2 : 1)>(p.n_qtiles);
     const int bh = tord.x;
     const int qt = p.n_qtiles - 1 - tord.y;  // longest causal rows first
     const int h = bh % p.H, b = bh / p.H;
@@ -903,10 +903,13 @@ hipError_t launch_fwd_t(const FwdParams& p, hipStream_t s) {
     // D = 32, no dropout, no bias), else into 2
     constexpr int KS_SMALL = (!Elem<T>::kF32 && D == 32 && DROPOUT == 0 && std::is_void<TB>::value) ? 4 : 2;
     const int n_cu = 256;
-    if (nblocks < n_cu && p.Sk > C::BN) {
-        hipLaunchKernelGGL((fwd_kernel<T, D, CAUSAL, DROPOUT, TB, KS_SMALL>), dim3((unsigned)nblocks),
-                           dim3(C::NT * KS_SMALL), 0, s, q);
-        return hipGetLastError();
+    // (D = 256: one workgroup's tiles take most of the LDS, no split)
+    if constexpr (D <= 128) {
+        if (nblocks < n_cu && p.Sk > C::BN) {
+            hipLaunchKernelGGL((fwd_kernel<T, D, CAUSAL, DROPOUT, TB, KS_SMALL>), dim3((unsigned)nblocks),
+                               dim3(C::NT * KS_SMALL), 0, s, q);
+            return hipGetLastError();
+        }
     }
     hipLaunchKernelGGL((fwd_kernel<T, D, CAUSAL, DROPOUT, TB, 1>), dim3((unsigned)nblocks), dim3(C::NT), 0, s, q);
     return hipGetLastError();
@@ -933,6 +936,24 @@ hipError_t launch_fwd_dispatch(const FwdParams& p, int D, bool causal, bool drop
 #undef FA_FWD_CASE
 #undef FA_FWD_MODES
     return hipErrorInvalidValue;
+}
+
+// Head dim 256 (16-bit inputs, no bias): one workgroup of 4 waves per CU, the
+// Q rows and O accumulators of a wave in 192 registers (translation units of
+// their own, fa_fwd_d256_*.hip).
+template <typename T>
+hipError_t launch_fwd_d256(const FwdParams& p, bool causal, bool dropout, hipStream_t s) {
+    static_assert(!Elem<T>::kF32, "16-bit inputs");
+    const int mode = !dropout ? 0 : (p.kb != nullptr ? 2 : 1);
+#define FA_FWD_MODES(CC)                                                    \
+    switch (mode) {                                                         \
+        case 0: return launch_fwd_t<T, 256, CC, 0, void>(p, s);             \
+        case 1: return launch_fwd_t<T, 256, CC, 1, void>(p, s);             \
+        default: return launch_fwd_t<T, 256, CC, 2, void>(p, s);            \
+    }
+    if (causal) FA_FWD_MODES(true)
+    FA_FWD_MODES(false)
+#undef FA_FWD_MODES
 }
 
 }  // namespace fa

@@ -138,6 +138,12 @@ hipError_t launch_bwd_bias_f16(const BwdParams& p, int D, bool causal, bool drop
 hipError_t launch_bwd_bias_f32(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
 hipError_t launch_bwd_bias32_bf16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
 hipError_t launch_bwd_bias32_f16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
+// head dim 256, 16-bit inputs without a bias: fa_{fwd,bwd}_d256_{bf16,f16}.hip
+// (D must be 256; the argument keeps the signature of the other launchers)
+hipError_t launch_fwd_d256_bf16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
+hipError_t launch_fwd_d256_f16(const FwdParams& p, int D, bool causal, bool dropout, hipStream_t s);
+hipError_t launch_bwd_d256_bf16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
+hipError_t launch_bwd_d256_f16(const BwdParams& p, int D, bool causal, bool dropout, int stage, hipStream_t s);
 // fa_misc.hip
 hipError_t launch_dropout_mask(uint64_t seed, uint64_t offset, int B, int H, int Sq, int Sk, float p,
                                uint8_t* keep, hipStream_t s);

@@ -19,8 +19,9 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfa_gfx950.so")
 ABI_VERSION = 2
-HEAD_DIMS = (32, 64, 128)  # compiled into the kernels
-MAX_HEAD_DIM = HEAD_DIMS[-1]
+HEAD_DIMS = (32, 64, 128)  # compiled into the kernels for every dtype, with or without a bias
+WIDE_HEAD_DIM = 256        # compiled for fp16 / bf16 inputs without a bias
+MAX_HEAD_DIM = WIDE_HEAD_DIM
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
@@ -157,16 +158,19 @@ def _strides(t: torch.Tensor):
     return _I64x4(*t.stride())
 
 
-def padded_head_dim(d: int) -> int:
-    """The compiled head dim a head dim of ``d`` (1..MAX_HEAD_DIM) runs at: the
-    smallest one >= d.  Zero columns added to q, k and v change no score (the
-    softmax scale is passed explicitly) and make the extra columns of O, dQ,
-    dK and dV exactly zero, so the results at d are those of a kernel built
-    for d; the dropout stream depends on (b, h, query, key) only, so the mask
-    is the same too.  0 for head dims with no kernel."""
+def padded_head_dim(d: int, dtype: Optional[torch.dtype] = None, bias: bool = False) -> int:
+    """The compiled head dim a head dim of ``d`` runs at: the smallest one >= d
+    (32, 64, 128; 256 for fp16 / bf16 inputs without a bias, when ``dtype`` is
+    given).  Zero columns added to q, k and v change no score (the softmax
+    scale is passed explicitly) and make the extra columns of O, dQ, dK and dV
+    exactly zero, so the results at d are those of a kernel built for d; the
+    dropout stream depends on (b, h, query, key) only, so the mask is the same
+    too.  0 for head dims with no kernel."""
     for hd in HEAD_DIMS:
         if 0 < d <= hd:
             return hd
+    if d <= WIDE_HEAD_DIM and dtype in (torch.float16, torch.bfloat16) and not bias:
+        return WIDE_HEAD_DIM
     return 0
 
 
@@ -292,7 +296,7 @@ def fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: 
     keep mask applied."""
     lib = load()
     D = q.shape[-1]
-    dp = padded_head_dim(D) or D  # no kernel: the library rejects it
+    dp = padded_head_dim(D, q.dtype, bias is not None) or D  # no kernel: the library rejects it
     q, k, v = (prepare(_pad_d(t, dp)) for t in (q, k, v))
     pb = _as_prepared(bias, q, k)
     B, Sq, H, _ = q.shape
@@ -340,7 +344,7 @@ def bwd(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float = 0.0,
     instead of regenerating it."""
     lib = load()
     D = q.shape[-1]
-    dp = padded_head_dim(D) or D
+    dp = padded_head_dim(D, q.dtype, bias is not None) or D
     q, k, v, o, do = (prepare(_pad_d(t, dp)) for t in (q, k, v, o, do))
     pb = _as_prepared(bias, q, k)
     if want_dbias and pb is None:
@@ -383,7 +387,7 @@ def bwd_static(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float
     by torch; the library call itself allocates nothing."""
     lib = load()
     D = q.shape[-1]
-    dp = padded_head_dim(D) or D
+    dp = padded_head_dim(D, q.dtype) or D
     q, k, v, o, do = (prepare(_pad_d(t, dp)) for t in (q, k, v, o, do))
     lse = lse.contiguous()
     dq = torch.empty_like(q, memory_format=torch.contiguous_format)

@@ -12,8 +12,9 @@ reference's ``utils.py:227-254`` scans cost a sync each).
 
 Fallback (reference ``interface.py:331-348, 453-490``): with
 ``fallback_on_error=True`` a request the gfx950 kernels do not implement
-(``NotImplementedError``: a head_dim above 128; smaller ones between the
-compiled 32 / 64 / 128 run zero-padded to the next) or reject as a
+(``NotImplementedError``: a head_dim above 256, or above 128 for float32
+inputs or with a bias; others between the compiled 32 / 64 / 128 / 256 run
+zero-padded to the next) or reject as a
 tile hint (``ValueError`` from ``block_size_m/n``) is served by PyTorch math on
 the same GPU, with a warning.  Everything else raises: a missing kernel library
 (:class:`FlashAttentionExtensionError`), a kernel error, CPU tensors (there is

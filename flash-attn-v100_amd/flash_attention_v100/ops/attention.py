@@ -52,16 +52,18 @@ def check_block_sizes(block_size_m: Optional[int], block_size_n: Optional[int]) 
             raise ValueError(f"{name}={val!r} is not a valid tile size (positive multiple of 16, <= 256)")
 
 
-def _check_kernel_inputs(q, k, v, dropout_p):
+def _check_kernel_inputs(q, k, v, dropout_p, bias=None):
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("Input tensors must be 4-dimensional [batch, seq_len, num_heads, head_dim]")
     if not (q.dtype == k.dtype == v.dtype) or q.dtype not in SUPPORTED_DTYPES:
         raise ValueError(f"dtype must be one of {SUPPORTED_DTYPES} and equal for q, k, v")
     if q.device.type != "cuda" or k.device != q.device or v.device != q.device:
         raise ValueError("Flash Attention requires q, k, v on the same GPU device")
-    if not _lib.padded_head_dim(q.shape[-1]):
-        raise NotImplementedError(f"head_dim {q.shape[-1]} has no kernel (1..{_lib.MAX_HEAD_DIM}; head dims "
-                                  f"between the compiled {_lib.HEAD_DIMS} run zero-padded to the next one)")
+    if not _lib.padded_head_dim(q.shape[-1], q.dtype, bias is not None):
+        raise NotImplementedError(
+            f"head_dim {q.shape[-1]} has no kernel for {q.dtype}{' with a bias' if bias is not None else ''} "
+            f"(1..{_lib.HEAD_DIMS[-1]}, and up to {_lib.WIDE_HEAD_DIM} for fp16 / bf16 without a bias; head dims "
+            f"between the compiled {_lib.HEAD_DIMS + (_lib.WIDE_HEAD_DIM,)} run zero-padded to the next one)")
     if k.shape != v.shape or k.shape[0] != q.shape[0] or k.shape[3] != q.shape[3]:
         raise ValueError(f"incompatible shapes q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
     if k.shape[2] == 0 or q.shape[2] % k.shape[2] != 0:
@@ -122,7 +124,7 @@ class EnhancedFlashAttentionV100Function(torch.autograd.Function):
         if enable_multi_gpu and world_size > 1:
             raise NotImplementedError("multi-GPU execution is out of scope for this single-GPU build")
         check_block_sizes(block_size_m, block_size_n)
-        _check_kernel_inputs(q, k, v, dropout_p)
+        _check_kernel_inputs(q, k, v, dropout_p, bias)
         if scale is None:
             scale = q.shape[-1] ** -0.5
         pb = _prepare_bias(bias, q, k)
@@ -190,12 +192,12 @@ FlashAttentionV100Function = EnhancedFlashAttentionV100Function
 # ---------------------------------------------------------------------------
 # Standalone functions (reference ops/attention.py:464-718) and their aliases
 
-def _standalone_inputs(q, k, v, scale, dropout_p, enable_multi_gpu, kwargs):
+def _standalone_inputs(q, k, v, scale, dropout_p, enable_multi_gpu, kwargs, bias=None):
     if enable_multi_gpu and torch.distributed.is_available() and torch.distributed.is_initialized() \
             and torch.distributed.get_world_size() > 1:
         raise NotImplementedError("multi-GPU execution is out of scope for this single-GPU build")
     check_block_sizes(kwargs.get("block_size_m"), kwargs.get("block_size_n"))
-    _check_kernel_inputs(q, k, v, dropout_p)
+    _check_kernel_inputs(q, k, v, dropout_p, bias)
     return q.shape[-1] ** -0.5 if scale is None else scale
 
 
@@ -214,7 +216,7 @@ def flash_attention_forward_enhanced(
     """Forward only, no autograd graph (reference ``ops/attention.py:464-536``):
     returns O (B, Sq, H, D).  ``dropout_seed`` / ``dropout_offset`` keyword
     arguments pin the dropout stream; ``block_size_m/n`` are validated hints."""
-    scale = _standalone_inputs(q, k, v, scale, dropout_p, enable_multi_gpu, kwargs)
+    scale = _standalone_inputs(q, k, v, scale, dropout_p, enable_multi_gpu, kwargs, bias)
     pb = _prepare_bias(bias, q, k)
     seed, offset = (_lib.seed_offset(kwargs.get("dropout_seed"), kwargs.get("dropout_offset"))
                     if dropout_p > 0 else (0, 0))
@@ -242,7 +244,7 @@ def flash_attention_backward_enhanced(
     bias passes the same ``dropout_p`` / ``dropout_seed`` / ``dropout_offset``
     / ``bias`` as keyword arguments."""
     dropout_p = float(kwargs.get("dropout_p", 0.0))
-    scale = _standalone_inputs(q, k, v, scale, dropout_p, enable_multi_gpu, kwargs)
+    scale = _standalone_inputs(q, k, v, scale, dropout_p, enable_multi_gpu, kwargs, kwargs.get("bias"))
     if dropout_p > 0 and kwargs.get("dropout_seed") is None:
         raise ValueError("dropout backward needs the forward's dropout_seed (and dropout_offset)")
     seed, offset = (_lib.seed_offset(kwargs.get("dropout_seed"), kwargs.get("dropout_offset"))
@@ -288,7 +290,7 @@ def compare_with_pytorch_attention_enhanced(
     applies the kernels' own keep mask (``fa_dropout_mask``) so that the two
     outputs are comparable element by element; the reference passed dropout
     to SDPA's independent RNG instead."""
-    _check_kernel_inputs(q, k, v, dropout_p)
+    _check_kernel_inputs(q, k, v, dropout_p, bias)
     scale = q.shape[-1] ** -0.5
     seed, offset = _lib.seed_offset(None, None) if dropout_p > 0 else (0, 0)
     flash = flash_attention_forward_enhanced(q, k, v, scale, causal, dropout_p, bias,

@@ -50,7 +50,7 @@ extern "C" {
 #define FA_OK 0
 #define FA_ERR_NULL_ARG -1    /* a required pointer is NULL */
 #define FA_ERR_SHAPE -2       /* a size is negative or inconsistent */
-#define FA_ERR_HEAD_DIM -3    /* head_dim not in {32, 64, 128} */
+#define FA_ERR_HEAD_DIM -3    /* head_dim not in {32, 64, 128}, nor 256 with 16-bit inputs and no bias */
 #define FA_ERR_DTYPE -4       /* dtype code not FA_DTYPE_* */
 #define FA_ERR_STRIDE -5      /* d stride != 1, or b/s/h stride not a multiple of 16 bytes */
 #define FA_ERR_HEADS -6       /* num_heads not a positive multiple of num_heads_kv */

@@ -196,6 +196,17 @@ static void fwd_rejects() {
     expect(t, FA_ERR_TOO_LARGE);
     t = a; t.seqlen_k = 1 << 28; expect(t, FA_ERR_TOO_LARGE);
     t = a; t.bias = alloc(64); t.bias_stride[2] = (int64_t)1 << 61; expect(t, FA_ERR_TOO_LARGE);
+    // head dim 256: 16-bit inputs without a bias only, on launchers of its own
+    fa_fwd_args w = make_fwd(1, 40, 40, 2, 2, 256, FA_DTYPE_BF16, 1);
+    CHECK(fa_fwd(&w, nullptr) == FA_OK);
+    CHECK(std::strcmp(g_stub.last, "launch_fwd_d256_bf16") == 0 && g_stub.D == 256);
+    w = make_fwd(1, 40, 40, 2, 2, 256, FA_DTYPE_F16, 0);
+    CHECK(fa_fwd(&w, nullptr) == FA_OK);
+    CHECK(std::strcmp(g_stub.last, "launch_fwd_d256_f16") == 0);
+    t = w; t.dtype = FA_DTYPE_F32; expect(t, FA_ERR_HEAD_DIM);
+    t = w; t.bias = alloc(40 * 40 * 2); t.bias_dtype = FA_DTYPE_F16; t.bias_stride[1] = 40 * 40; t.bias_stride[2] = 40;
+    expect(t, FA_ERR_HEAD_DIM);
+    t = w; t.head_dim = 192; expect(t, FA_ERR_HEAD_DIM);
 }
 
 static void bwd_paths() {
@@ -216,6 +227,13 @@ static void bwd_paths() {
         CHECK(fa_bwd_stage(&a, w, ws, s, nullptr) == FA_OK);
         CHECK(g_stub.stage == s);
     }
+    // head dim 256 (16-bit, no bias) on launchers of its own
+    fa_bwd_args a2 = make_bwd(1, 60, 60, 2, 1, 256, FA_DTYPE_F16, 1);
+    const size_t ws2 = fa_bwd_workspace_size(&a2);
+    CHECK(ws2 > 0 && fa_bwd(&a2, alloc(ws2), ws2, nullptr) == FA_OK);
+    CHECK(std::strcmp(g_stub.last, "launch_bwd_d256_f16") == 0 && g_stub.D == 256 && g_stub.stage == -1);
+    a2.dtype = FA_DTYPE_F32;
+    CHECK(fa_bwd_workspace_size(&a2) == 0 && fa_bwd_check(&a2, ws2) == FA_ERR_HEAD_DIM);
     // a bias gradient summed over the batch: parts in the workspace, then the reduction
     fa_bwd_args b = make_bwd(3, 70, 70, 4, 2, 128, FA_DTYPE_F16, 1);
     b.bias = alloc((size_t)4 * 70 * 72 * 2);

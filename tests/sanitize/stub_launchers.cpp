@@ -46,6 +46,10 @@ STUB_BWD(launch_bwd_bias_f16)
 STUB_BWD(launch_bwd_bias_f32)
 STUB_BWD(launch_bwd_bias32_bf16)
 STUB_BWD(launch_bwd_bias32_f16)
+STUB_FWD(launch_fwd_d256_bf16)
+STUB_FWD(launch_fwd_d256_f16)
+STUB_BWD(launch_bwd_d256_bf16)
+STUB_BWD(launch_bwd_d256_f16)
 
 hipError_t launch_dropout_mask(uint64_t, uint64_t, int, int, int, int, float, uint8_t*, hipStream_t) {
     g_stub.misc_calls++;

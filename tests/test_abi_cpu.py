@@ -131,9 +131,41 @@ def test_fwd_check_accepts_valid():
             assert _status(a) == CODES["FA_OK"]
 
 
+def test_head_dim_256_only_for_16_bit_inputs_without_bias():
+    for dt in (torch.float16, torch.bfloat16):
+        a, _ = _cpu_fwd(D=256, dtype=dt)
+        assert _status(a) == CODES["FA_OK"]
+    a, _ = _cpu_fwd(D=256, dtype=torch.float32)
+    assert _status(a) == CODES["FA_ERR_HEAD_DIM"]
+    # with a bias (forward and backward checks)
+    B, S, H, D = 1, 64, 2, 256
+    q = torch.zeros(B, S, H, D, dtype=torch.bfloat16)
+    lse = torch.zeros(B, H, S)
+    bias = torch.zeros(B, H, S, S, dtype=torch.bfloat16)
+    pb = _lib.prepare_bias(bias, B, H, S, S, torch.bfloat16)
+    a = _lib.fwd_args(q, q, q, q, lse, None, True, D ** -0.5, 0.0, 0, 0, pb)
+    assert _status(a) == CODES["FA_ERR_HEAD_DIM"]
+    lib = _lib.load()
+    ba = _lib.bwd_args(q, q, q, q, q, lse, q, q, q, True, D ** -0.5, 0.0, 0, 0, pb)
+    assert lib.fa_bwd_check(ctypes.byref(ba), 1 << 20) == CODES["FA_ERR_HEAD_DIM"]
+    ba = _lib.bwd_args(q, q, q, q, q, lse, q, q, q, True, D ** -0.5, 0.0, 0, 0)
+    assert lib.fa_bwd_check(ctypes.byref(ba), lib.fa_bwd_workspace_size(ctypes.byref(ba))) == CODES["FA_OK"]
+
+
+def test_padded_head_dim_rule():
+    assert [_lib.padded_head_dim(d) for d in (1, 32, 33, 64, 65, 128)] == [32, 32, 64, 64, 128, 128]
+    assert _lib.padded_head_dim(129) == 0 and _lib.padded_head_dim(256) == 0  # dtype unknown
+    for dt in (torch.float16, torch.bfloat16):
+        assert _lib.padded_head_dim(129, dt) == 256 and _lib.padded_head_dim(256, dt) == 256
+        assert _lib.padded_head_dim(257, dt) == 0 and _lib.padded_head_dim(200, dt, bias=True) == 0
+        assert _lib.padded_head_dim(100, dt, bias=True) == 128
+    assert _lib.padded_head_dim(200, torch.float32) == 0
+
+
 @pytest.mark.parametrize("field,value,code", [
     ("head_dim", 96, "FA_ERR_HEAD_DIM"),
-    ("head_dim", 256, "FA_ERR_HEAD_DIM"),
+    ("head_dim", 512, "FA_ERR_HEAD_DIM"),
+    ("head_dim", 192, "FA_ERR_HEAD_DIM"),
     ("dtype", 7, "FA_ERR_DTYPE"),
     ("batch", -1, "FA_ERR_SHAPE"),
     ("seqlen_k", -3, "FA_ERR_SHAPE"),

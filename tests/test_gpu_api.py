@@ -154,7 +154,7 @@ def test_causal_dropout_combinations_finite(causal, p):
 
 
 def test_kernel_errors_raise_not_fall_back():
-    q, k, v = _qkv((1, 64, 2, 256), torch.float16)  # no kernel for head_dim 256 (beyond 128)
+    q, k, v = _qkv((1, 64, 2, 320), torch.float16)  # no kernel for head_dim 320 (beyond 256)
     with pytest.warns(UserWarning, match="falling back"):
         fa.flash_attention_v100(q, k, v)
     with pytest.raises(NotImplementedError):
