@@ -73,6 +73,54 @@ void* static_scratch(hipStream_t s) {
     return ptr;
 }
 
+// A library-owned stream per GPU (default priority, non-blocking) with a fork
+// and a join event, for work of fa_bwd that runs beside the caller's stream:
+// created on first use with that GPU current; nullptr if any HIP call fails.
+// The caller holds g_side_mu from the fork to its join.
+struct SideStream {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+    bool tried = false;
+};
+std::mutex g_side_mu;
+SideStream g_side[kMaxDevices];
+
+int stream_device(hipStream_t s) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return -1;
+    if (s == nullptr) return cur;
+    hipDevice_t d;
+    if (hipStreamGetDevice(s, &d) != hipSuccess) return -1;
+    return (int)d;
+}
+
+SideStream* side_stream(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) return nullptr;
+    SideStream& ss = g_side[dev];
+    if (ss.tried) return ss.s ? &ss : nullptr;
+    ss.tried = true;
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+    if (dev != cur && hipSetDevice(dev) != hipSuccess) return nullptr;
+    hipStream_t st = nullptr;
+    hipEvent_t ef = nullptr, ej = nullptr;
+    bool ok = hipStreamCreateWithFlags(&st, hipStreamNonBlocking) == hipSuccess &&
+              hipEventCreateWithFlags(&ef, hipEventDisableTiming) == hipSuccess &&
+              hipEventCreateWithFlags(&ej, hipEventDisableTiming) == hipSuccess;
+    if (dev != cur) (void)hipSetDevice(cur);
+    if (!ok) {
+        if (ej) (void)hipEventDestroy(ej);
+        if (ef) (void)hipEventDestroy(ef);
+        if (st) (void)hipStreamDestroy(st);
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    ss.s = st;
+    ss.fork = ef;
+    ss.join = ej;
+    return &ss;
+}
+
 int elem_size(int32_t dtype) { return dtype == FA_DTYPE_F32 ? 4 : 2; }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -397,7 +445,13 @@ int32_t fa_bwd_check(const fa_bwd_args* a, size_t ws_bytes) {
     return FA_OK;
 }
 
-int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int32_t stage, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// fa_bwd_stage; `side` allows the whole backward (stage -1) to write the zero
+// tails of a causal bias gradient on the library's side stream
+int32_t bwd_run(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int32_t stage, void* stream, bool side) {
     if (stage < -1 || stage > 3) return FA_ERR_SHAPE;
     int32_t st = fa_bwd_check(a, ws_bytes);
     if (st) return st;
@@ -512,6 +566,24 @@ int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int
     const bool dropout = a->dropout_p > 0.f;
     hipStream_t s = (hipStream_t)stream;
     if (a->bias) {
+        // The zero tails of a causal gradient written in place (2.15 GB at
+        // B=4, H=32, S=4096 bf16) are pure HBM writes: in the whole backward
+        // they run on the side stream while the compute-bound dK/dV pass runs
+        // on the caller's, which waits for them (join) before it returns.
+        std::unique_lock<std::mutex> side_lock(g_side_mu, std::defer_lock);
+        SideStream* ss = nullptr;
+        if (side && stage < 0 && causal && p.dbias_zero_fill == 2) {
+            side_lock.lock();
+            ss = side_stream(stream_device(s));
+            if (ss) {
+                hipError_t e = hipEventRecord(ss->fork, s);
+                if (e == hipSuccess) e = hipStreamWaitEvent(ss->s, ss->fork, 0);
+                if (e == hipSuccess) e = fa::launch_dbias_zero_tails(p, ss->s);
+                if (e == hipSuccess) e = hipEventRecord(ss->join, ss->s);
+                if (e != hipSuccess) return status_of(e);
+                p.dbias_zero_fill = 3;
+            }
+        }
         const bool b32 = a->bias_dtype == FA_DTYPE_F32;
         const int D = a->head_dim;
         hipError_t e;
@@ -528,6 +600,12 @@ int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int
         }
         // the summed gradient follows the dK/dV stage (stream order)
         if (e == hipSuccess && reduce_db && (stage < 0 || stage == 1)) e = fa::launch_dbias_reduce(rp, s);
+        // join (also after a failed launch: nothing of this call may outlive it
+        // on the side stream unordered with the caller's stream)
+        if (p.dbias_zero_fill == 3) {
+            const hipError_t ej = hipStreamWaitEvent(s, ss->join, 0);
+            if (e == hipSuccess) e = ej;
+        }
         return status_of(e);
     }
     const bool d256 = a->head_dim == 256;
@@ -542,8 +620,16 @@ int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int
     }
 }
 
+}  // namespace
+
+extern "C" {
+
+int32_t fa_bwd_stage(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int32_t stage, void* stream) {
+    return bwd_run(a, workspace, ws_bytes, stage, stream, true);
+}
+
 int32_t fa_bwd(const fa_bwd_args* a, void* workspace, size_t ws_bytes, void* stream) {
-    return fa_bwd_stage(a, workspace, ws_bytes, -1, stream);
+    return bwd_run(a, workspace, ws_bytes, -1, stream, true);
 }
 
 int32_t fa_bwd_static(const fa_bwd_args* a, void* stream) {
@@ -557,7 +643,8 @@ int32_t fa_bwd_static(const fa_bwd_args* a, void* stream) {
         return FA_OK;
     void* ws = static_scratch((hipStream_t)stream);
     if (!ws) return FA_ERR_LAUNCH;
-    return fa_bwd_stage(a, ws, FA_BWD_STATIC_SCRATCH_BYTES, -1, stream);
+    // one stream only: no library stream or event is created on this path
+    return bwd_run(a, ws, FA_BWD_STATIC_SCRATCH_BYTES, -1, stream, false);
 }
 
 int32_t fa_dropout_mask(uint64_t seed, uint64_t offset, int32_t B, int32_t H, int32_t Sq, int32_t Sk,

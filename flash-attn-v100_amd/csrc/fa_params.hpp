@@ -79,7 +79,9 @@ struct BwdParams {
     // causal: who writes the zeros of the gradient that no kernel visits
     // (entries above the dK/dV blocks' first query tiles): 0 nobody (the
     // summed form, whose reduction writes them), 1 dkdv_kernel, element by
-    // element, 2 the dQ pass that reads dS (dq_from_ds), whole row tails
+    // element, 2 the dQ pass that reads dS (dq_from_ds), whole row tails, 3
+    // dbias_zero_tails_kernel (the same row tails, on a stream of their own
+    // beside the dK/dV pass)
     int dbias_zero_fill;
     // 1: the dQ pass reads dS from dbias (written by the dK/dV pass, dbias_es
     // bytes per element: the input dtype or float32) instead of recomputing
@@ -153,5 +155,8 @@ hipError_t launch_rand(uint64_t seed, const uint64_t* ctr, int64_t n, float* u, 
 // may be left unwritten
 hipError_t launch_keep_bits(const FwdParams& p, bool causal, hipStream_t s);
 hipError_t launch_dbias_reduce(const DbiasReduceParams& r, hipStream_t s);
+// the causal dBias zeros of dbias_zero_fill == 2 / 3 (dq_from_ds): for each
+// 128-query tile, keys from the tile's end on
+hipError_t launch_dbias_zero_tails(const BwdParams& p, hipStream_t s);
 
 }  // namespace fa

@@ -192,7 +192,14 @@ int32_t fa_bwd_check(const fa_bwd_args* args, size_t workspace_bytes);
 
 /* Backward: dq, dk, dv.  Replaces kernels/backward_kernel.py:208-318
  * (launch at :279-316).  workspace: >= fa_bwd_workspace_size bytes,
- * 256-byte aligned device memory. */
+ * 256-byte aligned device memory.  Stream-ordered on hip_stream.  With a
+ * causal bias gradient written in place (16-bit inputs, dS read back by the
+ * dQ pass), the zeros above each 128-query tile are written by a small kernel
+ * on a stream the library owns (one per GPU, default priority, created on
+ * first use), forked from hip_stream at entry and joined back to it before
+ * return, so that they overlap the dK/dV pass; callers see the same ordering
+ * as for any single-stream call.  fa_bwd_stage with stage -1 does the same;
+ * its single stages and fa_bwd_static write them on hip_stream. */
 int32_t fa_bwd(const fa_bwd_args* args, void* workspace, size_t workspace_bytes, void* hip_stream);
 
 /* One stage of fa_bwd: 0 = delta pre-pass (writes the workspace), 1 = dK/dV,

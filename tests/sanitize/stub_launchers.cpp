@@ -63,6 +63,10 @@ hipError_t launch_keep_bits(const FwdParams&, bool, hipStream_t) {
     g_stub.keep_bits_calls++;
     return hipSuccess;
 }
+hipError_t launch_dbias_zero_tails(const BwdParams&, hipStream_t) {
+    g_stub.misc_calls++;
+    return hipSuccess;
+}
 hipError_t launch_dbias_reduce(const DbiasReduceParams& r, hipStream_t) {
     g_stub.reduce = r;
     g_stub.reduce_calls++;

@@ -377,3 +377,48 @@ def test_bias_staged_forward(case):
         res = {"O": [maxabs(o[:, :, hh:hh + 1].cpu(), ro), maxabs(eo.cpu(), ro), ro.abs().max().item()],
                "LSE": [maxabs(lse[:, hh:hh + 1].cpu(), rl), maxabs(el.cpu(), rl), rl.abs().max().item()]}
         assert_parity(res, dt, f"staged head {hh}")
+
+
+def test_dbias_zero_tails_beside_dkdv_equal_staged():
+    """The whole backward with a causal bias gradient written in place writes
+    the gradient's zero row tails on the library's side stream, beside the
+    dK/dV pass, joined back to the caller's stream; run stage by stage the dQ
+    pass writes them.  Both must give the same bits, every element written,
+    from a non-default stream, on two calls in a row (the second smaller)."""
+    import ctypes
+    lib = _lib.load()
+    side = torch.cuda.Stream()
+    for B, S, H, D, dt in ((2, 640, 2, 128, torch.bfloat16), (1, 384, 3, 64, torch.float16)):
+        say(f"case: dbias zero tails on the side stream B={B} S={S} H={H} D={D} {dt}")
+        q, k, v, do = make_inputs(B, S, H, D, dt, seed=23)
+        bias = make_bias((B, H, S, S), dt)
+        scale = D ** -0.5
+        dev = [t.to(DEV) for t in (q, k, v, do)]
+        o, lse, _ = _lib.fwd(dev[0], dev[1], dev[2], True, scale, bias=bias.to(DEV))
+        pb = _lib.prepare_bias(bias.to(DEV), B, H, S, S, dt)
+        outs = []
+        for staged in (False, True):
+            dq, dk, dv = (torch.full_like(t, float("nan")) for t in dev[:3])
+            db = torch.full((B, H, S, S), float("nan"), device=DEV, dtype=dt)
+            a = _lib.bwd_args(dev[0], dev[1], dev[2], o, dev[3], lse, dq, dk, dv, True, scale, 0.0, 0, 0, pb, db)
+            nws = int(lib.fa_bwd_workspace_size(ctypes.byref(a)))
+            ws = torch.empty(max(nws, 256), device=DEV, dtype=torch.uint8)
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                sp = ctypes.c_void_p(side.cuda_stream)
+                wsp = ctypes.c_void_p(ws.data_ptr())
+                if staged:
+                    for stage in (0, 1, 2):
+                        st = lib.fa_bwd_stage(ctypes.byref(a), wsp, ws.numel(), stage, sp)
+                        assert st == 0, _lib.strerror(st)
+                else:
+                    st = lib.fa_bwd(ctypes.byref(a), wsp, ws.numel(), sp)
+                    assert st == 0, _lib.strerror(st)
+                # stream order: a reader on the caller's stream sees every zero
+                flat = db.view(-1)[: db.numel()].float().isnan().sum()
+            side.synchronize()
+            assert flat.item() == 0
+            outs.append((dq, dk, dv, db))
+        for x, y in zip(*outs):
+            assert torch.equal(x, y)
+        assert torch.equal(outs[0][3].tril(), outs[0][3])
