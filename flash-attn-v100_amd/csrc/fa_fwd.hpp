@@ -552,16 +552,19 @@ __global__ __launch_bounds__(256 * KS * QG, KS == 1 && QG == 1 && D <= 128 ? 2 :
 // so the two waves of a SIMD run one phase apart: while one issues its matrix
 // products, the other runs its softmax.  Every barrier is workgroup-wide.
 // K and V tiles (global -> LDS, read by all 8 waves) rotate through four
-// slots.  Waves 0-3 copy them: in the V phase of tile r each issues its share
-// of K(r+3) and V(r+2) (the same number of copy instructions per wave), after
-// waiting for its copies of two V phases ago, which the barrier closing the
-// phase then publishes; a copy thus has two rounds to land, and a slot is only
-// overwritten after both groups have read its previous tile.  Per query the arithmetic is that of fwd_kernel (same tile order,
-// same lazy rescale per 32-query wave), so the outputs are bit-identical to it.
+// slots.  A ninth wave only copies them (issuing a tile's 36 copy
+// instructions stalls the issuing wave for hundreds of cycles, which in a
+// compute wave lengthens its phase): in round r it copies K(r+3) after the
+// barrier that ends M(r) of waves 0-3 and V(r+2) after the one that ends
+// their V(r), once its copies of round r-2 have landed, which that second
+// barrier then publishes; a copy thus has two rounds to land, and a slot is
+// only overwritten after both groups have read its previous tile.  Per query
+// the arithmetic is that of fwd_kernel (same tile order, same lazy rescale per
+// 32-query wave), so the outputs are bit-identical to it.
 template <typename T, int D>
 struct FwdPPCfg {
-    static constexpr int NW = 8;
-    static constexpr int NT = 64 * NW;
+    static constexpr int NW = 8;                  // compute waves
+    static constexpr int NT = 64 * (NW + 1);      // threads: the compute waves and the copy wave
     static constexpr int BM = 32 * NW;            // queries per workgroup
     static constexpr int BN = 64;                 // keys per tile
     static constexpr int NB = BN / 32;            // 32-key blocks per tile
@@ -577,7 +580,7 @@ struct FwdPPCfg {
 };
 
 template <typename T, int D, bool CAUSAL>
-__global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const FwdParams p) {
+__global__ __launch_bounds__(576, 1) void fwd_pp_kernel(const FwdParams p) {
     using C = FwdPPCfg<T, D>;
     static_assert(!Elem<T>::kF32, "16-bit inputs");
     constexpr int BN = C::BN, NB = C::NB, KW = C::KW, VW = C::VW, NSLOT = C::NSLOT;
@@ -604,6 +607,42 @@ __global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const FwdParams p) {
     int kv_end = p.Sk;
     if (CAUSAL) kv_end = min(kv_end, min(q0 + C::BM, p.Sq));
     const int n_tiles = (kv_end + BN - 1) / BN;
+    T* Ks0 = smem;
+    T* Vs0 = smem + NSLOT * C::KTILE;
+
+    if (w == C::NW) {
+        // ---- the copy wave: the compute waves' barrier sequence, copies in between ----
+        // round r (barriers 2r+1, 2r+2 after the prologue's): K(r+3) replaces
+        // K(r-1) and V(r+2) replaces V(r-2), both last read in M(r-1), which
+        // both groups have finished.  Tiles past Sk read nothing and land as
+        // zeros.  At most 63 copy instructions are in flight (the vmcnt range).
+        DmaTile<T, BN, D, KW, 1> kd;
+        kd.init(p.k_ss, lane, 0);
+        DmaTile<T, BN, D, VW, 1> vd;
+        vd.init(p.v_ss, lane, 0);
+        constexpr int NKI = decltype(kd)::NI, NVI = decltype(vd)::NI;
+        static_assert(2 * NKI + NVI <= 63, "vmcnt range");
+        lds_barrier();
+        for (int r = 0; r <= n_tiles; ++r) {
+            const int j = r + 3;
+            barrier_no_fence();
+            // round r-2's K(r+1), V(r) have landed (only round r-1's copies may
+            // be in flight): the next barrier publishes them for M(r+1)
+            wait_vmem_below<NKI + NVI>();
+            kd.load_untracked(kbase + (int64_t)(j * BN) * p.k_ss, p.k_ss, p.Sk - j * BN,
+                              Ks0 + (j % NSLOT) * C::KTILE, lane);
+            barrier_no_fence();
+            wait_vmem_below<63 - NVI>();
+            vd.load_untracked(vbase + (int64_t)((j - 1) * BN) * p.v_ss, p.v_ss, p.Sk - (j - 1) * BN,
+                              Vs0 + ((j - 1) % NSLOT) * C::VTILE, lane);
+        }
+        barrier_no_fence();  // the one waves 0-3 pass after their last round
+        wait_vmem();         // every copy has landed before the slots hold O
+        lds_barrier();
+        lds_barrier();
+        return;
+    }
+
     // key tiles this wave uses, and how many of them need no mask
     int n_w = qw0 < p.Sq ? n_tiles : 0;
     if (CAUSAL) n_w = min(n_w, (qw0 + 31) / BN + 1);
@@ -628,9 +667,7 @@ __global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const FwdParams p) {
     float m_raw = -INFINITY;
     const float c = p.scale_log2;
 
-    T* Ks0 = smem;
-    T* Vs0 = smem + NSLOT * C::KTILE;
-    // prologue copies: all 8 waves; in the loop: waves 0-3, K(j) with V(j-1)
+    // prologue copies: the 8 compute waves (in the loop: the copy wave)
     DmaTile<T, BN, D, KW, C::NW> kdma;
     kdma.init(p.k_ss, lane, w);
     DmaTile<T, BN, D, VW, C::NW> vdma;
@@ -643,20 +680,7 @@ __global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const FwdParams p) {
         if (j < n_tiles)
             vdma.load(vbase + (int64_t)(j * BN) * p.v_ss, p.v_ss, p.Sk - j * BN, Vs0 + (j % NSLOT) * C::VTILE, lane);
     };
-    using Pair = DmaTilePair<T, BN, D, KW, VW, 4>;
-    Pair kvdma;
-    kvdma.init(p.k_ss, p.v_ss, lane, w & 3);
-    // K(j) and V(j - 1).  Issued whole even past the last tile (a tile past
-    // Sk has an empty buffer range: nothing is read and its slot, whose tile
-    // both groups have finished, fills with zeros), so that every batch of a
-    // wave has at least Pair::MIN_PER copy instructions.
-    auto dma_kv = [&](int j) FA_INLINE {
-        kvdma.load_untracked(kbase + (int64_t)(j * BN) * p.k_ss, p.k_ss, p.Sk - j * BN, Ks0 + (j % NSLOT) * C::KTILE,
-                             vbase + (int64_t)((j - 1) * BN) * p.v_ss, p.v_ss, p.Sk - (j - 1) * BN,
-                             Vs0 + ((j - 1) % NSLOT) * C::VTILE);
-    };
-
-    f32x16 s[NB];        // scores of tile r between its M and V phases
+    f32x16 s[NB];       // scores of tile r between its M and V phases
     s16x8 pk[BN / 16];   // P of tile r between its V phase and the M phase of tile r+1
 
     // ---- M phase of tile r: S(r) = K(r) Q^T, O^T += V(r-1)^T P(r-1) ----
@@ -769,8 +793,10 @@ __global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const FwdParams p) {
     };
 
     auto sched_fence = [&]() FA_INLINE { __builtin_amdgcn_sched_barrier(0); };
-    // one round: M phase, barrier, V phase (wait for the previous copies,
-    // issue the next ones), barrier
+    // one round: M phase, barrier, V phase, barrier (the copy wave issues the
+    // tile copies between them; no release fence: the copies are ordered by
+    // the copy wave's vmcnt waits, and every LDS read of M(r) has completed,
+    // its products consumed it)
     auto round = [&](int r, auto qk_tag, auto pv_tag, auto v_tag) FA_INLINE {
         sched_fence();
         if constexpr (decltype(qk_tag)::value || decltype(pv_tag)::value) mphase(r, qk_tag, pv_tag);
@@ -778,19 +804,7 @@ __global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const FwdParams p) {
         barrier_no_fence();
         sched_fence();
         if constexpr (decltype(v_tag)::value) vphase(r);
-        if (grp == 0) {
-            // this wave's copies of two V phases ago have landed (at most the
-            // last batch, >= MIN_PER instructions, is still in flight): the
-            // barrier below publishes them.  Then K(r+3) replaces K(r-1) and
-            // V(r+2) replaces V(r-2), both last read in M(r-1), which both
-            // groups have finished.
-            wait_vmem_below<Pair::MIN_PER>();
-            dma_kv(r + 3);
-        }
         sched_fence();
-        // no release fence: it would wait for the copies just issued.  The
-        // wait above orders this wave's landed copies before the barrier, and
-        // every LDS read of M(r) has completed (its products consumed it).
         barrier_no_fence();
     };
     using TT = std::true_type;
@@ -826,8 +840,7 @@ __global__ __launch_bounds__(512, 1) void fwd_pp_kernel(const FwdParams p) {
         p.lse[si] = l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
         if (p.mx) p.mx[si] = m_raw * p.scale;
     }
-    wait_vmem();     // no copy in flight (the last ones target unused slots)
-    lds_barrier();   // every wave is done with the K / V slots
+    lds_barrier();   // every wave is done with the K / V slots, every copy landed
     constexpr int OW = C::OW;
     T* Os = smem + w * 32 * OW;
 #pragma unroll

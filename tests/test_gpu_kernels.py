@@ -257,8 +257,10 @@ def test_bwd_stage3_equals_prepass_then_dq(dt, D):
 
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_bwd_stages_on_two_streams(with_bias):
-    # include/fa_abi.h: after stage 0, stages 1 (dK/dV [+ dBias]) and 2 (dQ) are
-    # independent and may run on two streams; results equal fa_bwd's bit for bit
+    # include/fa_abi.h: after stage 0, stages 1 (dK/dV) and 2 (dQ) are
+    # independent and may run on two streams when no bias gradient is asked
+    # for (a bias alone included); with one, stage 1 writes the dS that stage 2
+    # reads, so stage 2 follows stage 1.  Results equal fa_bwd's bit for bit.
     import ctypes
     say(f"case: fa_bwd_stage on two streams, bias={with_bias}")
     B, S, H, D = 2, 333, 4, 64
@@ -268,22 +270,25 @@ def test_bwd_stages_on_two_streams(with_bias):
         bias = torch.randn(1, H, S, S, device=DEV).to(torch.bfloat16)
         pb = _lib.prepare_bias(bias, B, H, S, S, torch.bfloat16)
     o, lse, _ = _lib.fwd(q, k, v, True, D ** -0.5, bias=pb)
-    ref = _lib.bwd(q, k, v, o, do, lse, True, D ** -0.5, bias=pb, want_dbias=with_bias)
     lib = _lib.load()
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    db = torch.empty(1, H, S, 336, device=DEV)[..., :S] if with_bias else None
-    a = _lib.bwd_args(q, k, v, o, do, lse, dq, dk, dv, True, D ** -0.5, 0.0, 0, 0, pb, db)
-    ws = torch.empty(lib.fa_bwd_workspace_size(ctypes.byref(a)), device=DEV, dtype=torch.uint8)
-    wsp = ctypes.c_void_p(ws.data_ptr())
-    s0, s1, s2 = torch.cuda.current_stream(), torch.cuda.Stream(), torch.cuda.Stream()
-    assert lib.fa_bwd_stage(ctypes.byref(a), wsp, ws.numel(), 0, ctypes.c_void_p(s0.cuda_stream)) == 0
-    s1.wait_stream(s0)
-    s2.wait_stream(s0)
-    assert lib.fa_bwd_stage(ctypes.byref(a), wsp, ws.numel(), 1, ctypes.c_void_p(s1.cuda_stream)) == 0
-    assert lib.fa_bwd_stage(ctypes.byref(a), wsp, ws.numel(), 2, ctypes.c_void_p(s2.cuda_stream)) == 0
-    s0.wait_stream(s1)
-    s0.wait_stream(s2)
-    torch.cuda.synchronize()
-    assert torch.equal(dq, ref[0]) and torch.equal(dk, ref[1]) and torch.equal(dv, ref[2])
-    if with_bias:
-        assert torch.equal(db.to(torch.bfloat16), ref[3])
+    for want_db in ((False, True) if with_bias else (False,)):
+        ref = _lib.bwd(q, k, v, o, do, lse, True, D ** -0.5, bias=pb, want_dbias=want_db)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        db = torch.empty(1, H, S, 336, device=DEV)[..., :S] if want_db else None
+        a = _lib.bwd_args(q, k, v, o, do, lse, dq, dk, dv, True, D ** -0.5, 0.0, 0, 0, pb, db)
+        ws = torch.empty(lib.fa_bwd_workspace_size(ctypes.byref(a)), device=DEV, dtype=torch.uint8)
+        wsp = ctypes.c_void_p(ws.data_ptr())
+        s0, s1, s2 = torch.cuda.current_stream(), torch.cuda.Stream(), torch.cuda.Stream()
+        assert lib.fa_bwd_stage(ctypes.byref(a), wsp, ws.numel(), 0, ctypes.c_void_p(s0.cuda_stream)) == 0
+        s1.wait_stream(s0)
+        s2.wait_stream(s0)
+        assert lib.fa_bwd_stage(ctypes.byref(a), wsp, ws.numel(), 1, ctypes.c_void_p(s1.cuda_stream)) == 0
+        if want_db:
+            s2.wait_stream(s1)  # dQ reads the dS stage 1 wrote
+        assert lib.fa_bwd_stage(ctypes.byref(a), wsp, ws.numel(), 2, ctypes.c_void_p(s2.cuda_stream)) == 0
+        s0.wait_stream(s1)
+        s0.wait_stream(s2)
+        torch.cuda.synchronize()
+        assert torch.equal(dq, ref[0]) and torch.equal(dk, ref[1]) and torch.equal(dv, ref[2])
+        if want_db:
+            assert torch.equal(db.to(torch.bfloat16), ref[3])
