@@ -868,16 +868,18 @@ __global__ __launch_bounds__(576, 1) void fwd_pp_kernel(const FwdParams p) {
     }
 }
 
-// When the ping-pong kernel runs (measured, D = 128): its 256-query
-// workgroups must fill the chip at least once, and with causal masking it
-// needs long rows and a grid that fills the chip four times (it runs one
-// workgroup per CU, so the causal diagonal, where the waves of the lower
-// query blocks have no work, and each workgroup's first tile copies are not
-// hidden by a second workgroup).  Causal, against fwd_kernel: 4096 tokens x
-// 128 (batch, head) -1.5%, 8192 x 32 -3.6%; 2048 x 128 +5%, 4096 x 16 +10%.
+// When the ping-pong kernel runs (measured, D = 128, bf16, interleaved A/B
+// against fwd_kernel): its 256-query workgroups must fill the chip at least
+// once, and with causal masking it needs long rows and a grid that fills the
+// chip twice (it runs one workgroup per CU, so the causal diagonal, where the
+// waves of the lower query blocks have no work, and each workgroup's first
+// tile copies are not hidden by a second workgroup).  Causal: (1, 4096, 32)
+// -12%, (1, 8192, 16) -14%, (2, 3072, 32) -6%; (1, 4096, 16) and (1, 8192, 8)
+// (256 workgroups) +3%, (4, 2048, 32) and (2, 2048, 64) equal, (8, 1024, 32)
+// +3%.
 inline bool fwd_pp_wanted(const FwdParams& p, bool causal) {
     const int64_t n = (int64_t)((p.Sq + 255) / 256) * p.H * p.B;
-    return n >= 256 && (!causal || (p.Sq >= 4096 && n >= 1024));
+    return n >= 256 && (!causal || (p.Sq >= 3072 && n >= 512));
 }
 
 template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
