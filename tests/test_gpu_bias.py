@@ -422,3 +422,55 @@ def test_dbias_zero_tails_beside_dkdv_equal_staged():
         for x, y in zip(*outs):
             assert torch.equal(x, y)
         assert torch.equal(outs[0][3].tril(), outs[0][3])
+
+
+def test_dbias_side_stream_from_two_threads():
+    """Two host threads, each on its own stream, run the whole backward with a
+    causal bias gradient (zero tails forked onto the library's one side
+    stream per GPU and joined back) several times at once; every result equals
+    the single-threaded one bit for bit."""
+    import ctypes
+    import threading
+    lib = _lib.load()
+    say("case: dbias zero tails on the side stream from two threads")
+    B, S, H, D, dt = 1, 512, 2, 64, torch.bfloat16
+    probs, refs = [], []
+    for seed in (41, 42):
+        q, k, v, do = (t.to(DEV) for t in make_inputs(B, S, H, D, dt, seed=seed))
+        bias = make_bias((B, H, S, S), dt, seed=seed).to(DEV)
+        o, lse, _ = _lib.fwd(q, k, v, True, D ** -0.5, bias=bias)
+        pb = _lib.prepare_bias(bias, B, H, S, S, dt)
+        refs.append(_lib.bwd(q, k, v, o, do, lse, True, D ** -0.5, bias=pb, want_dbias=True))
+        probs.append((q, k, v, o, do, lse, pb))
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(i):
+        try:
+            q, k, v, o, do, lse, pb = probs[i]
+            st = torch.cuda.Stream()
+            st.wait_stream(torch.cuda.default_stream())
+            with torch.cuda.stream(st):
+                for rep in range(4):
+                    dq, dk, dv = (torch.full_like(t, float("nan")) for t in (q, k, v))
+                    db = torch.full((B, H, S, S), float("nan"), device=DEV, dtype=dt)
+                    a = _lib.bwd_args(q, k, v, o, do, lse, dq, dk, dv, True, D ** -0.5, 0.0, 0, 0, pb, db)
+                    ws = torch.empty(max(int(lib.fa_bwd_workspace_size(ctypes.byref(a))), 256), device=DEV,
+                                     dtype=torch.uint8)
+                    code = lib.fa_bwd(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                      ctypes.c_void_p(st.cuda_stream))
+                    if code != 0:
+                        raise RuntimeError(_lib.strerror(code))
+                    st.synchronize()
+                    if not all(torch.equal(x, y) for x, y in zip((dq, dk, dv, db), refs[i])):
+                        raise AssertionError(f"thread {i} call {rep} differs from the single-threaded result")
+        except Exception as e:  # reported by the main thread
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(probs))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads), "a worker did not finish"
+    assert not errors, errors
