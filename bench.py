@@ -333,8 +333,11 @@ def copy_calibration(gib: float = 1.0, reps: int = 5):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # 30 untimed steps bring the clocks to their steady state under this load:
+    # after only 5 the first timed steps run slower (C3 on one box: 2.39-2.41 ms
+    # per step against 2.347 after 30, the latter equal to the event-timed step)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--bias", choices=("none", "full", "heads"), default="none",
                     help="run the additive-bias path: full = (B, H, S, S), heads = (1, H, S, S), bf16")
