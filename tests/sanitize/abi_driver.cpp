@@ -255,6 +255,24 @@ static void bwd_paths() {
     CHECK(g_stub.reduce_calls == r0 + 1 && g_stub.reduce.sum_b == 1 && g_stub.reduce.sum_h == 0);
     CHECK(g_stub.reduce.SkP == 72 && g_stub.bwd.dbias_dtype == FA_DTYPE_F32 && g_stub.bwd.dbias_zero_fill == 0);
     CHECK(std::strcmp(g_stub.last, "launch_bwd_bias_f16") == 0);
+    // a causal gradient written in place (dS read back by the dQ pass): the whole
+    // backward writes the zero tails on the library's side stream when it can
+    // create one; without a device (here) it cannot, and the dQ pass writes them
+    fa_bwd_args c = make_bwd(2, 64, 64, 2, 2, 64, FA_DTYPE_BF16, 1);
+    c.bias = alloc((size_t)2 * 2 * 64 * 64 * 2);
+    c.bias_dtype = FA_DTYPE_BF16;
+    c.bias_stride[0] = 2 * 64 * 64;
+    c.bias_stride[1] = 64 * 64;
+    c.bias_stride[2] = 64;
+    c.dbias = alloc((size_t)2 * 2 * 64 * 64 * 2);
+    c.dbias_dtype = FA_DTYPE_BF16;
+    c.dbias_stride[0] = 2 * 64 * 64;
+    c.dbias_stride[1] = 64 * 64;
+    c.dbias_stride[2] = 64;
+    const size_t wsc = fa_bwd_workspace_size(&c);
+    CHECK(fa_bwd(&c, alloc(wsc), wsc, nullptr) == FA_OK);
+    CHECK(g_stub.bwd.dq_from_ds == 1 && g_stub.bwd.dbias_zero_fill == 2 && g_stub.stage == -1);
+    CHECK(std::strcmp(g_stub.last, "launch_bwd_bias_bf16") == 0);
     // rejections
     fa_bwd_args t = a; t.dq = nullptr; CHECK(fa_bwd_check(&t, ws) == FA_ERR_NULL_ARG);
     t = a; t.dbias = alloc(64); CHECK(fa_bwd_check(&t, ws) == FA_ERR_BIAS);  // dbias without a bias
