@@ -480,6 +480,426 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
 }
 
 // ---------------------------------------------------------------------------
+// Ping-pong dK/dV for 16-bit inputs without bias or dropout, D = 128, on grids
+// that fill the CUs.  One workgroup = 8 waves = 256 keys of one (batch, KV
+// head), one workgroup per CU; wave w owns the 32 keys k0 + 32 w ..., whose K
+// and V rows it holds in registers (as dkdv_kernel's waves do).  The 64-query
+// tiles of Q, dO, LSE * log2 e and delta are consumed as two 32-query
+// sub-steps, one per round; every wave runs, for each round r,
+//   M(r): dV += dO^T P(r-1), dK += Q^T dS(r-1), then S(r) = Q K^T, dP(r) = dO V^T
+//   V(r): P(r) = exp2(S c - LSE), dS(r) = P (dP - delta), packed to 16 bits
+// with a workgroup barrier after each phase, but waves 4-7 pass one extra
+// barrier first (and waves 0-3 one at the end).  Waves w and w + 4 share a
+// SIMD (the hardware deals the waves of a workgroup to SIMDs 0, 2, 1, 3, 0, 2,
+// 1, 3), so the two run one phase apart: one's matrix products overlap the
+// other's softmax arithmetic.
+// Tile copies (direct to LDS) stall the issuing wave while the CU's vector
+// memory path takes them (about 64 bytes a clock), so they are spread thin:
+// each tile is shared by 256 keys, and each wave issues 3 copy instructions
+// in each of its V phases -- waves 0-3 the Q rows and LSE row of tile
+// (r + 3) / 2, waves 4-7 the dO rows and delta row of tile (r + 4) / 2 (one
+// half of the tile's 24 instructions per round, the LSE / delta row copied
+// twice so every wave issues the same number).  Tiles rotate through three
+// LDS slots: tile j replaces tile j - 3, whose last reader, the M phase of
+// round 2 j - 4 of waves 4-7, precedes the first copy of tile j (V phase of
+// round 2 j - 4 of waves 4-7, round 2 j - 3 of waves 0-3).  At the end of its
+// V phase a wave waits until its copies of earlier rounds have landed, which
+// covers tile j before the barrier that opens M(2 j) of waves 0-3.  Per
+// element the arithmetic is that of dkdv_kernel, in the same order (each
+// key's dK / dV accumulate its query tiles in the same sequence), so the
+// outputs are bit-identical to it.
+template <typename T, int D>
+struct DkdvPPCfg {
+    static constexpr int NW = 8;
+    static constexpr int NT = 64 * NW;
+    static constexpr int BK = 32 * NW;               // keys per workgroup
+    static constexpr int BQ = 64;                    // queries per tile: two 32-query sub-steps
+    static constexpr int RW = D + 24;                // Q / dO row stride, as in dkdv_kernel
+    static constexpr int QALLOC = BQ * RW * (int)sizeof(T);
+    // per slot: Q rows, dO rows, then LSE * log2 e [BQ] and delta [BQ] as floats
+    static constexpr int SLOT_BYTES = 2 * QALLOC + 2 * BQ * 4;
+    static constexpr int NSLOT = 3;
+    static constexpr int SMEM_BYTES = NSLOT * SLOT_BYTES;
+    static constexpr int EPC = 16 / (int)sizeof(T);
+    static constexpr int CW = RW / EPC;              // 16-byte chunks per LDS row
+    static constexpr int NI = BQ * CW / 64;          // copy instructions per tile and matrix (all 64 lanes)
+    static_assert((BQ * CW) % 64 == 0, "whole copy instructions");
+    // a group's items per tile: NI row copies + the LSE / delta row, dealt as
+    // item 8 n + 4 hf + w4 to wave w4 of the group in the V phase of half hf:
+    // 3 items per wave in half 0, 2 in half 1
+    static_assert(NI + 1 == 20, "20 items per group and tile");
+    static constexpr int OW = D + 8;                 // output staging row stride
+    static_assert(SMEM_BYTES <= 160 * 1024, "LDS of one CU");
+    static_assert(NW * 32 * OW * (int)sizeof(T) <= SMEM_BYTES, "output staging");
+    static_assert(SLOT_BYTES % 16 == 0, "16-byte aligned slots");
+};
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, const int n_ktiles) {
+    using C = DkdvPPCfg<T, D>;
+    static_assert(!Elem<T>::kF32 && D == 128, "16-bit inputs, D = 128");
+    constexpr int BQ = C::BQ, RW = C::RW;
+    __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
+    const int grp = w >> 2, w4 = w & 3;
+    const int2 tord = tile_order<32>(n_ktiles);
+    const int bhk = tord.x;
+    const int kt = tord.y;
+    const int hk = bhk % p.Hkv, b = bhk / p.Hkv;
+    const int k0 = kt * C::BK;
+    const int kw0 = k0 + 32 * w;
+    const int kj = kw0 + l32;  // this lane's key
+
+    // ---- K, V rows of this lane's key in registers (MFMA B operands) ----
+    constexpr int KR = D / 16;
+    uint4 kreg[KR], vreg[KR];
+    {
+        const T* krow = (const T*)p.k + b * p.k_sb + (int64_t)kj * p.k_ss + hk * p.k_sh;
+        const T* vrow = (const T*)p.v + b * p.v_sb + (int64_t)kj * p.v_ss + hk * p.v_sh;
+        const bool ok = kj < p.Sk;
+#pragma unroll
+        for (int i = 0; i < KR; ++i) {
+            const int d0 = 16 * i + 8 * hi;
+            kreg[i] = ok ? *reinterpret_cast<const uint4*>(krow + d0) : make_uint4(0u, 0u, 0u, 0u);
+            vreg[i] = ok ? *reinterpret_cast<const uint4*>(vrow + d0) : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    f32x16 dk[D / 32], dv[D / 32];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) { dk[i] = f32x16{}; dv[i] = f32x16{}; }
+    const float c = p.scale_log2;
+
+    // the run of tiles: per query head of the KV group, the query tiles from
+    // the last one down to the first that reaches the workgroup's keys (as in
+    // dkdv_kernel: the workgroups of a head read the same tiles together)
+    const int qt_begin = CAUSAL ? (k0 / BQ) : 0;
+    const int qt_end = (p.Sq + BQ - 1) / BQ;
+    const int nq = qt_end > qt_begin ? qt_end - qt_begin : 0;
+    const int total = nq * p.group;  // tiles; rounds = 2 * total
+    // position of a tile in the run (head in group, tile in the head's run,
+    // LDS slot), advanced one tile at a time: no integer division in the loop
+    struct Pos {
+        int h, i, s;
+    };
+    auto advance = [&](Pos& t) FA_INLINE {
+        if (++t.i == nq) {
+            t.i = 0;
+            ++t.h;
+        }
+        if (++t.s == C::NSLOT) t.s = 0;
+    };
+    auto pos_q0 = [&](const Pos& t) FA_INLINE { return (qt_end - 1 - t.i) * BQ; };
+    auto pos_head = [&](const Pos& t) FA_INLINE { return hk * p.group + t.h; };
+    auto slot = [&](int s) FA_INLINE -> char* { return smem + s * C::SLOT_BYTES; };
+    // this wave's sub-step (first query qs0): any visible (query, key) pair,
+    // and any masked one
+    auto active = [&](int qs0) FA_INLINE { return !CAUSAL || qs0 + 31 >= kw0; };
+    auto masked = [&](int qs0) FA_INLINE { return CAUSAL && qs0 < kw0 + 31; };
+
+    // ---- tile copies: waves 0-3 Q rows (+ LSE), waves 4-7 dO rows (+ delta) ----
+    // The wave's source base, strides and the workspace base are formed once
+    // and kept opaque (scalar registers): otherwise the compiler re-reads the
+    // kernel arguments inside the loop (a scalar memory load and a wait for
+    // it, and for every LDS access in flight, per round).
+    auto opaque64 = [](uint64_t x) FA_INLINE {
+        asm volatile("" : "+s"(x));
+        return x;
+    };
+    auto opaque32 = [](uint32_t x) FA_INLINE {
+        asm volatile("" : "+s"(x));
+        return x;
+    };
+    const int64_t css = grp == 0 ? p.q_ss : p.do_ss;  // row stride (elements)
+    const uint64_t cbase = opaque64((uint64_t)(uintptr_t)(grp == 0 ? (const T*)p.q + b * p.q_sb
+                                                                   : (const T*)p.dout + b * p.do_sb));
+    const uint64_t crow = opaque64((uint64_t)css * sizeof(T));                             // bytes per row
+    const uint64_t chead = opaque64((uint64_t)(grp == 0 ? p.q_sh : p.do_sh) * sizeof(T));  // bytes per head
+    const uint64_t wbase = opaque64((uint64_t)(uintptr_t)(p.lse2 + (int64_t)b * p.H * p.ws_stride));
+    const uint32_t wrow_bytes = opaque32((uint32_t)p.ws_stride * 4u);
+    const uint32_t full_bytes = opaque32((uint32_t)(((BQ - 1) * (int)css + D) * (int)sizeof(T)));
+    const uint32_t woff = 4u * (uint32_t)(grp * p.sq_pad + lane);
+    const int q_rows = p.Sq;
+    // per-lane source offsets of the wave's row-copy items 8 n + 4 hf + w4
+    // (instruction g covers LDS chunks 64 g ..; padding chunks read nothing)
+    int coff[2][3];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int n = 0; n < 3; ++n) {
+            const int cidx = 64 * (8 * n + 4 * hf + w4) + lane;
+            const int row = cidx / C::CW, col = cidx % C::CW;
+            coff[hf][n] = col < D / C::EPC ? (row * (int)css + col * C::EPC) * (int)sizeof(T) : kOffNowhere;
+        }
+    // half hf of tile t (slot): the wave's items 8 n + 4 hf + w4 of the group's 20
+    auto issue = [&](const Pos& t, int hf) FA_INLINE {
+        const int hh = pos_head(t), qb0 = pos_q0(t);
+        char* sp = slot(t.s);
+        // the tile's rows [0, min(Sq - qb0, BQ)); rows past it land as zeros
+        const int nv = q_rows - qb0;
+        const uint32_t bytes = nv >= BQ ? full_bytes : (uint32_t)(((nv - 1) * (int)css + D) * (int)sizeof(T));
+        const uint64_t src = cbase + (uint64_t)(int64_t)qb0 * crow + (uint64_t)hh * chead;
+        u32x4 rs;
+        rs[0] = (uint32_t)src;
+        rs[1] = (uint32_t)(src >> 32) & 0xFFFFu;
+        rs[2] = bytes;
+        rs[3] = 0x00020000u;
+        // (scalar: M0 takes the LDS address; computed with vector ops, it
+        // would not be accepted as the asm's scalar operand)
+        const uint32_t l0 = __builtin_amdgcn_readfirstlane(lds_addr(sp + grp * C::QALLOC));
+        auto items = [&](auto hf_tag) FA_INLINE {
+            constexpr int HF = decltype(hf_tag)::value;
+#pragma unroll
+            for (int n = 0; n < 3; ++n) {
+                const int g = 8 * n + 4 * HF + w4;  // wave-uniform
+                if (g < C::NI) {
+                    dma_load16_untracked(rs, __builtin_amdgcn_readfirstlane(l0 + 1024 * g), coff[HF][n]);
+                } else if (g == C::NI) {  // the LSE (waves 0-3) or delta (waves 4-7) row, one dword per lane
+                    const uint64_t wsrc = wbase + (uint64_t)hh * wrow_bytes + 4u * (uint32_t)qb0;  // qb0 + BQ <= sq_pad
+                    u32x4 ws;
+                    ws[0] = (uint32_t)wsrc;
+                    ws[1] = (uint32_t)(wsrc >> 32) & 0xFFFFu;
+                    ws[2] = wrow_bytes - 4u * (uint32_t)qb0;
+                    ws[3] = 0x00020000u;
+                    dma_load4_untracked(ws, __builtin_amdgcn_readfirstlane(lds_addr(sp + 2 * C::QALLOC + grp * 4 * BQ)),
+                                        woff);
+                }
+            }
+        };
+        if (hf == 0)
+            items(std::integral_constant<int, 0>{});
+        else
+            items(std::integral_constant<int, 1>{});
+    };
+
+    // ---- M phase: dV/dK of the previous sub-step, then S/dP of this one ----
+    // dV/dK step t (t = ks (D / 32) + i): dO^T, Q^T of query rows 16 ks .. of
+    // the sub-step, d block i (transposing reads); S/dP step kk: the Q, dO row
+    // fragments d = 16 kk + 8 hi of query row l32.  The LDS operands of step
+    // t + MP are read during step t.
+    const int trow = 4 * hi + ((lane & 15) >> 2);
+    const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    constexpr int NA = 2 * (D / 32);  // dV/dK steps (a dV and a dK product each)
+    constexpr int NSTEP = NA + D / 16;
+    constexpr int MP = 2;
+    s16x8 bp8[2], bs8[2];  // P, dS of the previous sub-step (B operands)
+    f32x16 sc, dpc;
+    // A: dV/dK of the sub-step in slot sa / rows sta; BB: S/dP of the one in slot sb / rows stb
+    auto mphase = [&](int sa, int sta, int sb, int stb, auto a_tag, auto b_tag) FA_INLINE {
+        constexpr bool A = decltype(a_tag)::value, BB = decltype(b_tag)::value;
+        const T* Qa = (const T*)slot(sa) + 32 * sta * RW;
+        const T* Da = (const T*)(slot(sa) + C::QALLOC) + 32 * sta * RW;
+        const T* Qb = (const T*)slot(sb) + (32 * stb + l32) * RW + 8 * hi;
+        const T* Db = (const T*)(slot(sb) + C::QALLOC) + (32 * stb + l32) * RW + 8 * hi;
+        s16x8 x[NSTEP], y[NSTEP];
+        auto rd = [&](int t) FA_INLINE {
+            if (t < NA) {
+                const int ks = t / (D / 32), i = t % (D / 32);
+                const int off = (16 * ks + trow) * RW + 32 * i + tcol;
+                x[t] = cat4(lds_read_tr16(Da + off), lds_read_tr16(Da + off + 8 * RW));
+                y[t] = cat4(lds_read_tr16(Qa + off), lds_read_tr16(Qa + off + 8 * RW));
+            } else {
+                const int kk = t - NA;
+                x[t] = *reinterpret_cast<const s16x8*>(Qb + 16 * kk);
+                y[t] = *reinterpret_cast<const s16x8*>(Db + 16 * kk);
+            }
+        };
+        auto mm = [&](int t) FA_INLINE {
+            if (t < NA) {
+                const int ks = t / (D / 32), i = t % (D / 32);
+                dv[i] = Elem<T>::mfma(x[t], bp8[ks], dv[i]);
+                dk[i] = Elem<T>::mfma(y[t], bs8[ks], dk[i]);
+            } else {
+                const int kk = t - NA;
+                sc = Elem<T>::mfma(x[t], __builtin_bit_cast(s16x8, kreg[kk]), kk == 0 ? f32x16{} : sc);
+                dpc = Elem<T>::mfma(y[t], __builtin_bit_cast(s16x8, vreg[kk]), kk == 0 ? f32x16{} : dpc);
+            }
+        };
+        constexpr int T0 = A ? 0 : NA, T1 = BB ? NSTEP : NA;
+#pragma unroll
+        for (int t = T0; t < T0 + MP; ++t) rd(t);
+#pragma unroll
+        for (int t = T0; t < T1; ++t) {
+            if (t + MP < T1) rd(t + MP);
+            mm(t);
+        }
+        // the same order for the scheduler: reads of MP steps, then per step
+        // its two products followed by the reads of step t + MP
+        auto rd_group = [&](int t) FA_INLINE {  // 4 transposing reads or 2 row reads
+            if (t < NA)
+                __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            else
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        };
+#pragma unroll
+        for (int t = T0; t < T0 + MP; ++t) rd_group(t);
+#pragma unroll
+        for (int t = T0; t < T1; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            if (t + MP < T1) rd_group(t + MP);
+        }
+    };
+
+    // ---- V phase: P, dS of the sub-step (rows st of the tile in slot s) ----
+    // On a sub-step that straddles the diagonal (msk), the entries of queries
+    // below this lane's key are then zeroed in place (one code path: branches
+    // that each produce P / dS make the register allocator spill)
+    auto vphase = [&](int s, int st, int qs0, bool msk) FA_INLINE {
+        const float* lse2 = (const float*)(slot(s) + 2 * C::QALLOC) + 32 * st;
+        const float* dels = lse2 + BQ;
+        float pd[16], ds[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse2 + 8 * g + 4 * hi);
+            const f32x4 d4 = *reinterpret_cast<const f32x4*>(dels + 8 * g + 4 * hi);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int rr = 4 * g + e;
+                const float pv = fast_exp2(__builtin_fmaf(sc[rr], c, -l4[e]));
+                pd[rr] = pv;
+                ds[rr] = pv * (dpc[rr] - d4[e]);
+            }
+        }
+        if (CAUSAL && msk) {
+            // query qs0 + 8 g + 4 hi + e is masked when 8 g + e < dlt (one
+            // per-lane value against constants)
+            const int dlt = kj - 4 * hi - qs0;
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (8 * g + e < dlt) {
+                        pd[4 * g + e] = 0.f;
+                        ds[4 * g + e] = 0.f;
+                    }
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            bp8[ks] = pack8<T>(pd + 8 * ks);
+            bs8[ks] = pack8<T>(ds + 8 * ks);
+        }
+    };
+
+    auto sched_fence = [&]() FA_INLINE { __builtin_amdgcn_sched_barrier(0); };
+    using TT = std::true_type;
+    using FF = std::false_type;
+
+    // prologue: tiles 0 and 1, every wave its group's 6 instructions of each
+    {
+        Pos t{0, 0, 0};
+        for (int j = 0; j < 2; ++j) {
+            if (j < total) {
+                issue(t, 0);
+                issue(t, 1);
+            }
+            advance(t);
+        }
+    }
+    wait_vmem();
+    lds_barrier();
+    if (grp == 1) barrier_no_fence();  // waves 4-7 run one phase behind
+
+    // V phase of round r (tile pr, sub-step st): this round's copies -- half
+    // (m & 1) of tile m / 2, m = r + 3 (waves 0-3) or r + 4 (waves 4-7), tiles
+    // 2 .. total - 1 (the prologue copied 0 and 1) -- then P, dS (zero where
+    // the sub-step has no visible pair or there is no sub-step), then wait for
+    // this wave's copies of earlier rounds.
+    Pos pc{0, 0, 0};  // tile m / 2 of the copies
+    advance(pc);
+    if (grp == 1) advance(pc);  // round 0: tile 1 (waves 0-3, nothing to copy) or 2 (waves 4-7)
+    auto vround = [&](int r, const Pos& pr, int st, bool act) FA_INLINE {
+        const int m = r + 3 + grp;
+        const int j = m >> 1;
+        const bool cp = j >= 2 && j < total;
+        if (cp) issue(pc, m & 1);
+        if (m & 1) advance(pc);
+        if (act) {
+            const int qs0 = pos_q0(pr) + 32 * st;
+            vphase(pr.s, st, qs0, masked(qs0));
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                bp8[ks] = s16x8{};
+                bs8[ks] = s16x8{};
+            }
+        }
+        if (!cp)
+            wait_vmem();
+        else if ((m & 1) == 0)
+            wait_vmem_below<3>();
+        else
+            wait_vmem_below<2>();
+    };
+    // Round 0 runs S/dP only; rounds 1 .. 2 total run both halves of the M
+    // phase unconditionally (one code path keeps the accumulators in place): a
+    // sub-step without visible pairs gets P = dS = 0, and the S/dP products of
+    // round 2 total (no sub-step) are not used.  Idle products cost no time,
+    // as the workgroup's waves run in lock step.
+    if (total > 0) {
+        Pos pr{0, 0, 0};  // tile of round r
+        sched_fence();
+        mphase(0, 0, 0, 0, FF{}, TT{});
+        sched_fence();
+        barrier_no_fence();
+        sched_fence();
+        vround(0, pr, 0, active(pos_q0(pr)));
+        sched_fence();
+        barrier_no_fence();
+        int s_prev = 0;
+        for (int r = 1; r <= 2 * total; ++r) {
+            const int st = r & 1;
+            if (st == 0) advance(pr);
+            sched_fence();
+            mphase(s_prev, st ^ 1, pr.s, st, TT{}, TT{});
+            sched_fence();
+            barrier_no_fence();
+            sched_fence();
+            vround(r, pr, st, r < 2 * total && active(pos_q0(pr) + 32 * st));
+            sched_fence();
+            barrier_no_fence();
+            s_prev = pr.s;
+        }
+    }
+    if (grp == 0) barrier_no_fence();
+    sched_fence();
+
+    // ---- epilogue: stage dK^T, dV^T through LDS as rows, coalesced stores ----
+    // (every M phase is done: the last barrier follows M(2 total) of waves 4-7)
+    constexpr int OW = C::OW;
+    constexpr int EPC = 16 / sizeof(T);
+    constexpr int CPR = D / EPC;
+    T* Os = reinterpret_cast<T*>(smem) + w * 32 * OW;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        if (pass == 1) lds_barrier();  // this wave's dK rows are stored (its own region)
+        const f32x16* acc = pass == 0 ? dk : dv;
+        const float mul = pass == 0 ? p.scale : 1.f;
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                s16x4 v4;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v4[e] = Elem<T>::pack1(acc[i][4 * g + e] * mul);
+                *reinterpret_cast<s16x4*>(Os + l32 * OW + 32 * i + 8 * g + 4 * hi) = v4;
+            }
+        lds_barrier();
+        T* gbase = pass == 0 ? (T*)p.dk + b * p.dk_sb + hk * p.dk_sh : (T*)p.dv + b * p.dv_sb + hk * p.dv_sh;
+        const int64_t gss = pass == 0 ? p.dk_ss : p.dv_ss;
+#pragma unroll
+        for (int i = 0; i < 32 * CPR / 64; ++i) {
+            const int cidx = lane + 64 * i;
+            const int row = cidx / CPR, col = cidx % CPR;
+            const int key = kw0 + row;
+            if (key < p.Sk)
+                *reinterpret_cast<uint4*>(gbase + (int64_t)key * gss + col * EPC) =
+                    *reinterpret_cast<const uint4*>(Os + row * OW + col * EPC);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // dK/dV with K and V in LDS (16-bit inputs, D >= 64, no dropout): for grids
 // of fewer workgroups than CUs, and with a bias at every grid size (the
 // bias's registers do not fit two workgroups of dkdv_kernel per CU at D = 128).
@@ -1233,6 +1653,355 @@ __global__ __launch_bounds__(256 * KS, (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)) 
 }
 
 // ---------------------------------------------------------------------------
+// Ping-pong dQ for 16-bit inputs without bias or dropout, D = 128, on grids
+// that fill the CUs.  One workgroup = 8 waves = 256 queries of one (batch,
+// head), one workgroup per CU, like the ping-pong forward: waves w and w + 4
+// share a SIMD and own the adjacent 32-query blocks 2 (w % 4) and 2 (w % 4) + 1
+// (similar causal lengths); Q, dO (and O, for delta) of the wave's queries sit
+// in registers.  64-key tiles of K and V rotate through four LDS slots.  Every
+// wave runs, for each key tile r,
+//   M(r): dQ^T += K(r-1)^T dS^T(r-1), then S^T(r) = K Q^T, dP^T(r) = V dO^T
+//   V(r): P = exp2(S c - LSE), dS = P (dP - delta), packed to 16 bits
+// with a workgroup barrier after each phase; waves 4-7 run one phase behind,
+// so one wave's 48 matrix products overlap the other's arithmetic.  The tile
+// copies (direct to LDS) go in the V phases: waves 0-3 copy K(r + 2), waves
+// 4-7 V(r + 3) in round r (4 or 5 copy instructions each); a slot is refilled
+// only after both groups' M phases that read its previous tile, and a wave's
+// copies have landed before the barrier that opens the first M phase reading
+// them (the schedule of dkdv_pp_kernel's first version, checked on the host).
+// Per query the arithmetic is that of dq_kernel, in the same order (delta and
+// LSE * log2 e computed as there and written to the workspace rows for the
+// dK/dV pass), so dQ and the workspace rows are bit-identical to it.
+template <typename T, int D>
+struct DqPPCfg {
+    static constexpr int NW = 8;
+    static constexpr int NT = 64 * NW;
+    static constexpr int BM = 32 * NW;               // queries per workgroup
+    static constexpr int BN = 64;                    // keys per tile
+    static constexpr int KW = D + 24;                // K / V row stride, as in dq_kernel
+    static constexpr int KALLOC = BN * KW * (int)sizeof(T);
+    static constexpr int SLOT_BYTES = 2 * KALLOC;    // K rows, V rows
+    static constexpr int NSLOT = 4;
+    static constexpr int SMEM_BYTES = NSLOT * SLOT_BYTES;
+    static constexpr int EPC = 16 / (int)sizeof(T);
+    static constexpr int CW = KW / EPC;              // 16-byte chunks per LDS row
+    static constexpr int NI = BN * CW / 64;          // copy instructions per tile and matrix
+    static_assert((BN * CW) % 64 == 0, "whole copy instructions");
+    static constexpr int PER = (NI + 3) / 4;         // per wave of a group (at most)
+    static constexpr int OW = D + 8;                 // output staging row stride
+    static_assert(SMEM_BYTES <= 160 * 1024, "LDS of one CU");
+    static_assert(NW * 32 * OW * (int)sizeof(T) <= SMEM_BYTES, "output staging");
+};
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void dq_pp_kernel(const BwdParams p) {
+    using C = DqPPCfg<T, D>;
+    static_assert(!Elem<T>::kF32 && D == 128, "16-bit inputs, D = 128");
+    constexpr int BN = C::BN, KW = C::KW, NSLOT = C::NSLOT;
+    __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
+    const int grp = w >> 2, w4 = w & 3;
+    const int blk = 2 * w4 + grp;
+    const int n_qtiles = (p.Sq + C::BM - 1) / C::BM;
+    const int2 tord = tile_order<32>(n_qtiles);
+    const int bh = tord.x;
+    const int qt = n_qtiles - 1 - tord.y;  // longest causal rows first
+    const int h = bh % p.H, b = bh / p.H;
+    const int hk = h / p.group;
+    const int q0 = qt * C::BM;
+    const int qw0 = q0 + 32 * blk;
+    const int qi = qw0 + l32;
+
+    // ---- Q, dO (and O) rows of this lane's query in registers (MFMA B operands) ----
+    constexpr int QR = D / 16;
+    const bool own_delta = p.dq_delta != 0;
+    uint4 qreg[QR], doreg[QR], oreg[QR];
+    {
+        const T* qrow = (const T*)p.q + b * p.q_sb + (int64_t)qi * p.q_ss + h * p.q_sh;
+        const T* drow = (const T*)p.dout + b * p.do_sb + (int64_t)qi * p.do_ss + h * p.do_sh;
+        const T* orow = (const T*)p.o + b * p.o_sb + (int64_t)qi * p.o_ss + h * p.o_sh;
+        const bool ok = qi < p.Sq;
+#pragma unroll
+        for (int i = 0; i < QR; ++i) {
+            const int d0 = 16 * i + 8 * hi;
+            qreg[i] = ok ? *reinterpret_cast<const uint4*>(qrow + d0) : make_uint4(0u, 0u, 0u, 0u);
+            doreg[i] = ok ? *reinterpret_cast<const uint4*>(drow + d0) : make_uint4(0u, 0u, 0u, 0u);
+        }
+        if (own_delta) {
+#pragma unroll
+            for (int i = 0; i < QR; ++i)
+                oreg[i] = ok ? *reinterpret_cast<const uint4*>(orow + 16 * i + 8 * hi) : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    // the workspace rows hold sq_pad (Sq rounded up to 128) entries; the last
+    // 256-query block may reach past them (its queries past Sq get P = 0)
+    const bool in_ws = qi < p.sq_pad;
+    const int64_t wi = ((int64_t)b * p.H + h) * p.ws_stride + qi;
+    float lse2 = INFINITY, del = 0.f, lse_in = 0.f;
+    if (own_delta)
+        lse_in = qi < p.Sq ? p.lse[((int64_t)b * p.H + h) * p.Sq + qi] : -INFINITY;
+    else if (in_ws) {
+        lse2 = p.lse2[wi];
+        del = p.delta[wi];
+    }
+    const float c = p.scale_log2;
+    f32x16 dq[D / 32];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) dq[i] = f32x16{};
+
+    int kv_end = p.Sk;
+    if (CAUSAL) kv_end = min(kv_end, min(q0 + C::BM, p.Sq));
+    const int n_tiles = (kv_end + BN - 1) / BN;
+    // key tiles this wave uses, and how many of them need no mask
+    int n_w = qw0 < p.Sq ? n_tiles : 0;
+    if (CAUSAL) n_w = min(n_w, (qw0 + 31) / BN + 1);
+    int n_um = min(n_w, p.Sk / BN);
+    if (CAUSAL) n_um = min(n_um, (qw0 + 1) / BN);
+
+    // ---- K / V tile copies: waves 0-3 K, waves 4-7 V (instructions w4, w4 + 4, ...) ----
+    auto opaque64 = [](uint64_t x) FA_INLINE {
+        asm volatile("" : "+s"(x));
+        return x;
+    };
+    const int64_t css = grp == 0 ? p.k_ss : p.v_ss;
+    const uint64_t cbase = opaque64((uint64_t)(uintptr_t)(grp == 0 ? (const T*)p.k + b * p.k_sb + hk * p.k_sh
+                                                                   : (const T*)p.v + b * p.v_sb + hk * p.v_sh));
+    const uint64_t crow = opaque64((uint64_t)css * sizeof(T));
+    const uint32_t full_bytes = (uint32_t)(((BN - 1) * (int)css + D) * (int)sizeof(T));
+    const int n_copy = (C::NI - w4 + 3) / 4;  // this wave's instructions per tile (wave-uniform)
+    int coff[C::PER];
+#pragma unroll
+    for (int t = 0; t < C::PER; ++t) {
+        const int cidx = 64 * (w4 + 4 * t) + lane;
+        const int row = cidx / C::CW, col = cidx % C::CW;
+        // padding chunks of an LDS row read nothing (out of the buffer's range)
+        coff[t] = col < D / C::EPC ? (row * (int)css + col * C::EPC) * (int)sizeof(T) : kOffNowhere;
+    }
+    auto slot = [&](int r) FA_INLINE -> char* { return smem + (r & (NSLOT - 1)) * C::SLOT_BYTES; };
+    static_assert(NSLOT == 4, "slot index by mask");
+    auto issue = [&](int j) FA_INLINE {
+        const int k0 = j * BN;
+        const int nv = p.Sk - k0;  // > 0: j < n_tiles
+        const uint32_t bytes = nv >= BN ? full_bytes : (uint32_t)(((nv - 1) * (int)css + D) * (int)sizeof(T));
+        const uint64_t src = cbase + (uint64_t)(int64_t)k0 * crow;
+        u32x4 rs;
+        rs[0] = (uint32_t)src;
+        rs[1] = (uint32_t)(src >> 32) & 0xFFFFu;
+        rs[2] = bytes;
+        rs[3] = 0x00020000u;
+        const uint32_t l0 = __builtin_amdgcn_readfirstlane(lds_addr(slot(j) + grp * C::KALLOC));
+#pragma unroll
+        for (int t = 0; t < C::PER; ++t) {
+            const int g = w4 + 4 * t;  // wave-uniform
+            if (g < C::NI) dma_load16_untracked(rs, __builtin_amdgcn_readfirstlane(l0 + 1024 * g), coff[t]);
+        }
+    };
+
+    // ---- M phase: dQ^T of the previous tile, then S^T / dP^T of this one ----
+    // dQ step t (t = ks (D / 32) + i, ks = 16-key step of the 64): K^T of keys
+    // 16 ks + ..., d block i (transposing reads of the K tile); S/dP step
+    // t = 2 kk + kb: the K, V row fragments d = 16 kk + 8 hi of key 32 kb + l32.
+    const int trow = 4 * hi + ((lane & 15) >> 2);
+    const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    constexpr int NA = (BN / 16) * (D / 32);  // dQ steps (one product each)
+    constexpr int NB = 2 * QR;                // S/dP steps (an S and a dP product each)
+    constexpr int NSTEP = NA + NB;
+    constexpr int MP = 2;
+    s16x8 bs8[BN / 16];       // dS^T of the previous tile (B operands)
+    f32x16 sc[2], dpc[2];     // S^T, dP^T of this tile, per 32-key block
+    auto mphase = [&](int r, auto a_tag, auto b_tag) FA_INLINE {
+        constexpr bool A = decltype(a_tag)::value, BB = decltype(b_tag)::value;
+        const T* Ka = (const T*)slot(r + NSLOT - 1);
+        const T* Kb = (const T*)slot(r) + l32 * KW + 8 * hi;
+        const T* Vb = (const T*)(slot(r) + C::KALLOC) + l32 * KW + 8 * hi;
+        s16x8 x[NSTEP], y[NSTEP];
+        auto rd = [&](int t) FA_INLINE {
+            if (t < NA) {
+                const int ks = t / (D / 32), i = t % (D / 32);
+                const T* kp = Ka + (16 * ks + trow) * KW + 32 * i + tcol;
+                x[t] = cat4(lds_read_tr16(kp), lds_read_tr16(kp + 8 * KW));
+            } else {
+                const int u = t - NA, kk = u >> 1, kb = u & 1;
+                x[t] = *reinterpret_cast<const s16x8*>(Kb + 32 * kb * KW + 16 * kk);
+                y[t] = *reinterpret_cast<const s16x8*>(Vb + 32 * kb * KW + 16 * kk);
+            }
+        };
+        auto mm = [&](int t) FA_INLINE {
+            if (t < NA) {
+                const int ks = t / (D / 32), i = t % (D / 32);
+                dq[i] = Elem<T>::mfma(x[t], bs8[ks], dq[i]);
+            } else {
+                const int u = t - NA, kk = u >> 1, kb = u & 1;
+                sc[kb] = Elem<T>::mfma(x[t], __builtin_bit_cast(s16x8, qreg[kk]), kk == 0 ? f32x16{} : sc[kb]);
+                dpc[kb] = Elem<T>::mfma(y[t], __builtin_bit_cast(s16x8, doreg[kk]), kk == 0 ? f32x16{} : dpc[kb]);
+            }
+        };
+        constexpr int T0 = A ? 0 : NA, T1 = BB ? NSTEP : NA;
+#pragma unroll
+        for (int t = T0; t < T0 + MP; ++t) rd(t);
+#pragma unroll
+        for (int t = T0; t < T1; ++t) {
+            if (t + MP < T1) rd(t + MP);
+            mm(t);
+        }
+        // the same order for the scheduler: reads of MP steps, then per step
+        // its products followed by the reads of step t + MP
+        auto rd_group = [&](int t) FA_INLINE {  // 2 transposing reads, or 2 row reads
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        };
+        auto mf_group = [&](int t) FA_INLINE {
+            if (t < NA)
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            else
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        };
+#pragma unroll
+        for (int t = T0; t < T0 + MP; ++t) rd_group(t);
+#pragma unroll
+        for (int t = T0; t < T1; ++t) {
+            mf_group(t);
+            if (t + MP < T1) rd_group(t + MP);
+        }
+    };
+
+    // ---- V phase of tile r: dS^T = P^T (dP^T - delta), packed (mask: diagonal / tail tiles) ----
+    auto vphase = [&](int r, bool msk) FA_INLINE {
+        float ds[2][16];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float pv = fast_exp2(__builtin_fmaf(sc[kb][e], c, -lse2));
+                ds[kb][e] = pv * (dpc[kb][e] - del);
+            }
+        if (msk) {
+            // key r BN + 32 kb + 8 g + 4 hi + f (e = 4 g + f) is masked when it
+            // is >= Sk or (causal) > qi: one per-lane bound against constants
+            const int kbase = r * BN + 4 * hi;
+            const int lim = CAUSAL ? min(p.Sk - 1, qi) - kbase : p.Sk - 1 - kbase;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    if (32 * kb + 8 * (e >> 2) + (e & 3) > lim) ds[kb][e] = 0.f;
+        }
+#pragma unroll
+        for (int ks = 0; ks < BN / 16; ++ks) bs8[ks] = pack8<T>(&ds[ks >> 1][8 * (ks & 1)]);
+    };
+
+    auto sched_fence = [&]() FA_INLINE { __builtin_amdgcn_sched_barrier(0); };
+    using TT = std::true_type;
+    using FF = std::false_type;
+
+    // prologue: tiles 0, 1, 2 (every wave its instructions of each)
+    for (int j = 0; j < 3; ++j)
+        if (j < n_tiles) issue(j);
+    if (own_delta) {
+        // delta = rowsum(dO * O) as dq_kernel computes it (16-byte chunk sums,
+        // then a pairwise tree, then the lane pair), written to the workspace
+        // with LSE * log2 e; rows past Sq: delta = 0, LSE * log2 e = +inf
+        float cs[QR];
+#pragma unroll
+        for (int i = 0; i < QR; ++i) {
+            const s16x8 a = __builtin_bit_cast(s16x8, oreg[i]), d = __builtin_bit_cast(s16x8, doreg[i]);
+            float acc = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc += Elem<T>::unpack1(a[e]) * Elem<T>::unpack1(d[e]);
+            cs[i] = acc;
+        }
+#pragma unroll
+        for (int st = QR / 2; st > 0; st >>= 1)
+#pragma unroll
+            for (int i = 0; i < st; ++i) cs[i] = cs[i] + cs[i + st];
+        del = pair_sum(cs[0]);
+        lse2 = lse_in == -INFINITY ? INFINITY : lse_in * kLog2e;
+        if (hi == 0 && in_ws) {
+            p.lse2[wi] = lse2;
+            p.delta[wi] = del;
+        }
+    }
+    wait_vmem();
+    lds_barrier();
+    if (grp == 1) barrier_no_fence();  // waves 4-7 run one phase behind
+
+    // V phase of round r: this round's copies (tile r + 2 + grp; tiles 0-2 came
+    // with the prologue), then dS of tile r (zero where the wave has no tile r),
+    // then wait for this wave's copies of earlier rounds
+    auto vround = [&](int r) FA_INLINE {
+        const int j = r + 2 + grp;
+        const bool cp = j >= 3 && j < n_tiles;
+        if (cp) issue(j);
+        if (r < n_w)
+            vphase(r, r >= n_um);
+        else {
+#pragma unroll
+            for (int ks = 0; ks < BN / 16; ++ks) bs8[ks] = s16x8{};
+        }
+        if (!cp)
+            wait_vmem();
+        else if (n_copy == C::PER)
+            wait_vmem_below<C::PER>();
+        else
+            wait_vmem_below<C::PER - 1>();
+    };
+    // Round 0 runs S/dP only; rounds 1 .. n_tiles run both halves of the M
+    // phase unconditionally (one code path keeps the accumulators in place):
+    // a wave past its last tile gets dS = 0, and the S/dP products of round
+    // n_tiles (no tile) are not used.
+    if (n_tiles > 0) {
+        sched_fence();
+        mphase(0, FF{}, TT{});
+        sched_fence();
+        barrier_no_fence();
+        sched_fence();
+        vround(0);
+        sched_fence();
+        barrier_no_fence();
+        for (int r = 1; r <= n_tiles; ++r) {
+            sched_fence();
+            mphase(r, TT{}, TT{});
+            sched_fence();
+            barrier_no_fence();
+            sched_fence();
+            vround(r);
+            sched_fence();
+            barrier_no_fence();
+        }
+    }
+    if (grp == 0) barrier_no_fence();
+    sched_fence();
+
+    // ---- epilogue: stage dQ^T through LDS as rows, coalesced stores ----
+    // (every M phase is done: the last barrier follows the last M phase of waves 4-7)
+    constexpr int OW = C::OW;
+    T* Os = reinterpret_cast<T*>(smem) + w * 32 * OW;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            s16x4 v4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v4[e] = Elem<T>::pack1(dq[i][4 * g + e] * p.scale);
+            *reinterpret_cast<s16x4*>(Os + l32 * OW + 32 * i + 8 * g + 4 * hi) = v4;
+        }
+    lds_barrier();
+    constexpr int EPC = 16 / sizeof(T);
+    constexpr int CPR = D / EPC;
+    T* gbase = (T*)p.dq + b * p.dq_sb + h * p.dq_sh;
+#pragma unroll
+    for (int i = 0; i < 32 * CPR / 64; ++i) {
+        const int cidx = lane + 64 * i;
+        const int row = cidx / CPR, col = cidx % CPR;
+        const int q = qw0 + row;
+        if (q < p.Sq)
+            *reinterpret_cast<uint4*>(gbase + (int64_t)q * p.dq_ss + col * EPC) =
+                *reinterpret_cast<const uint4*>(Os + row * OW + col * EPC);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // dQ from the stored dS (16-bit inputs with a bias gradient requested).  The
 // dK/dV pass writes dS = P (dP - delta) of every (query, key) it visits into
 // the gradient buffer (per batch and head; ES bytes per element: the input
@@ -1446,6 +2215,21 @@ inline bool dkdv8_runs(const BwdParams& p) {
     return false;
 }
 
+// Whether the dK/dV stage runs dkdv_pp_kernel (16-bit inputs, D = 128, no
+// bias or dropout): one 8-wave workgroup per CU, so the grid must fill the CUs.
+inline bool dkdv_pp_runs(const BwdParams& p) {
+    const int64_t nb = (int64_t)((p.Sk + 255) / 256) * p.Hkv * p.B;
+    return nb >= 256;
+}
+
+// Whether the dQ stage runs dq_pp_kernel (16-bit inputs, D = 128, no bias or
+// dropout): one 8-wave workgroup of 256 queries per CU, so the grid must fill
+// the CUs.
+inline bool dq_pp_runs(const BwdParams& p) {
+    const int64_t nb = (int64_t)((p.Sq + 255) / 256) * p.H * p.B;
+    return nb >= 256;
+}
+
 template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
 hipError_t launch_bwd_t(const BwdParams& p0, int stage, hipStream_t s) {
     // stage 3: the workspace rows and dQ, for a dQ pass that recomputes dS.
@@ -1479,9 +2263,18 @@ hipError_t launch_bwd_t(const BwdParams& p0, int stage, hipStream_t s) {
         const int nk = (p.Sk + C::BK - 1) / C::BK;
         const int64_t nb = (int64_t)nk * p.Hkv * p.B;
         bool done = false;
+        if constexpr (!Elem<T>::kF32 && DROPOUT == 0 && std::is_void<TB>::value && D == 128) {
+            if (dkdv_pp_runs(p)) {
+                using CP = DkdvPPCfg<T, D>;
+                const int nk2 = (p.Sk + CP::BK - 1) / CP::BK;
+                const int64_t nb2 = (int64_t)nk2 * p.Hkv * p.B;
+                hipLaunchKernelGGL((dkdv_pp_kernel<T, D, CAUSAL>), dim3((unsigned)nb2), dim3(CP::NT), 0, s, p, nk2);
+                done = true;
+            }
+        }
         if constexpr (!Elem<T>::kF32 && DROPOUT == 0 && D >= 64 && D <= 128) {
             static_assert(Dkdv8Cfg<T, D>::BK == C::BK, "same key blocks");
-            if (dkdv8_runs<T, D, CAUSAL, DROPOUT, TB>(p)) {
+            if (!done && dkdv8_runs<T, D, CAUSAL, DROPOUT, TB>(p)) {
                 hipLaunchKernelGGL((dkdv8_kernel<T, D, CAUSAL, TB>), dim3((unsigned)nb), dim3(Dkdv8Cfg<T, D>::NT), 0, s, p,
                                    nk);
                 done = true;
@@ -1506,6 +2299,14 @@ hipError_t launch_bwd_t(const BwdParams& p0, int stage, hipStream_t s) {
                     else
                         hipLaunchKernelGGL((dq_ds_kernel<T, D, CAUSAL, 2>), dim3((unsigned)nb), dim3(256), 0, s, p, nq, fill);
                 }
+                done = true;
+            }
+        }
+        if constexpr (!Elem<T>::kF32 && DROPOUT == 0 && std::is_void<TB>::value && D == 128) {
+            if (!done && dq_pp_runs(p)) {
+                using CP = DqPPCfg<T, D>;
+                const int64_t nb2 = (int64_t)((p.Sq + CP::BM - 1) / CP::BM) * p.H * p.B;
+                hipLaunchKernelGGL((dq_pp_kernel<T, D, CAUSAL>), dim3((unsigned)nb2), dim3(CP::NT), 0, s, p);
                 done = true;
             }
         }
