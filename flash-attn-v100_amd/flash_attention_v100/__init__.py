@@ -32,6 +32,8 @@ from .ops.attention import (  # noqa: F401
     flash_attention_forward,
 )
 from .modules import EnhancedMultiHeadAttention  # noqa: F401
+from .config import DebugConfig  # noqa: F401
+from .utils import check_tensor_nan_inf  # noqa: F401
 
 __version__ = "0.1.0"
 
@@ -54,4 +56,6 @@ __all__ = [
     "flash_attention_forward",
     "flash_attention_backward",
     "compare_with_pytorch_attention",
+    "DebugConfig",
+    "check_tensor_nan_inf",
 ]

@@ -196,30 +196,57 @@ class PreparedBias:
     """An additive bias in the layout the kernels read: ``tensor`` viewed as
     (B, H, Sq, Sk) with zero strides on broadcast dimensions, key stride 1,
     other strides multiples of 16 bytes, 16-byte aligned base; element type the
-    input dtype or float32.  ``shape`` and ``dtype`` are the caller's, for the
-    gradient."""
+    input dtype or float32.  ``shape`` is the bias's shape as a 4-D view (size 1
+    on broadcast dimensions), ``dtype`` its dtype and ``caller_shape`` the shape
+    it was given in (2-D, 3-D or 4-D): the gradient is returned in it."""
 
-    __slots__ = ("tensor", "strides", "dtype_code", "shape", "dtype")
+    __slots__ = ("tensor", "strides", "dtype_code", "shape", "dtype", "caller_shape")
 
-    def __init__(self, tensor, strides, dtype_code, shape, dtype):
+    def __init__(self, tensor, strides, dtype_code, shape, dtype, caller_shape=None):
         self.tensor, self.strides, self.dtype_code, self.shape, self.dtype = tensor, strides, dtype_code, shape, dtype
+        self.caller_shape = tuple(shape) if caller_shape is None else tuple(caller_shape)
 
 
-def prepare_bias(bias: torch.Tensor, B: int, H: int, Sq: int, Sk: int, dtype: torch.dtype) -> PreparedBias:
-    """Validate a (B|1, H|1, Sq|1, Sk) bias (the reference's shapes,
-    ops/attention.py:58 and forward_kernel.py:166-182, plus a broadcast query
-    dimension) and bring it into the kernels' layout.  A bias in the input dtype
-    or float32 is read as it is; any other dtype is converted to float32 (exact
-    for float16/bfloat16), so the bias is added in fp32 as the reference's Triton
-    kernel did.  Rows are copied into a 16-byte padded buffer only when the
-    given strides or base do not meet the kernels' alignment."""
-    if not isinstance(bias, torch.Tensor) or bias.dim() != 4:
-        raise ValueError("bias must be a 4-D tensor [batch|1, heads|1, seq_len_q|1, seq_len_k]")
+BIAS_SHAPES_DOC = "[batch|1, heads|1, seq_len_q|1, seq_len_k], [heads, seq_len_q, seq_len_k] or [seq_len_q, seq_len_k]"
+
+
+def bias_as_4d(bias: torch.Tensor, B: int, H: int, Sq: int, Sk: int) -> torch.Tensor:
+    """The bias as a 4-D view: (B|1, H|1, Sq|1, Sk) as it is, (H, Sq, Sk) as
+    (1, H, Sq, Sk) and (Sq, Sk) as (1, 1, Sq, Sk) -- the shapes the reference's
+    validator accepts (``utils.py:204-211``; its 3-D form is heads-first, "no
+    batch dim").  Raises ``ValueError`` for any other shape."""
+    if not isinstance(bias, torch.Tensor) or bias.dim() not in (2, 3, 4):
+        raise ValueError(f"bias must be a tensor of shape {BIAS_SHAPES_DOC}")
     shape = tuple(bias.shape)
+    if bias.dim() == 2:
+        if shape != (Sq, Sk):
+            raise ValueError(f"bias shape {shape} not compatible with attention shape. Expected {(Sq, Sk)} "
+                             f"for a 2-D (position) bias")
+        return bias.unsqueeze(0).unsqueeze(0)
+    if bias.dim() == 3:
+        if shape != (H, Sq, Sk):
+            raise ValueError(f"bias shape {shape} not compatible with attention shape. Expected {(H, Sq, Sk)} "
+                             f"for a 3-D (per-head) bias")
+        return bias.unsqueeze(0)
     want = (B, H, Sq, Sk)
     for d in range(4):
         if shape[d] not in (1, want[d]):
             raise ValueError(f"bias shape {shape} is not broadcastable to {want}")
+    return bias
+
+
+def prepare_bias(bias: torch.Tensor, B: int, H: int, Sq: int, Sk: int, dtype: torch.dtype) -> PreparedBias:
+    """Validate a (B|1, H|1, Sq|1, Sk), (H, Sq, Sk) or (Sq, Sk) bias (the
+    reference's shapes, utils.py:204-211 and forward_kernel.py:166-182, plus a
+    broadcast query dimension) and bring it into the kernels' layout.  A bias
+    in the input dtype or float32 is read as it is; any other dtype is converted
+    to float32 (exact for float16/bfloat16), so the bias is added in fp32 as the
+    reference's Triton kernel did.  Rows are copied into a 16-byte padded
+    buffer only when the given strides or base do not meet the kernels'
+    alignment."""
+    caller_shape = tuple(bias.shape) if isinstance(bias, torch.Tensor) else None
+    bias = bias_as_4d(bias, B, H, Sq, Sk)
+    shape = tuple(bias.shape)
     orig_dtype = bias.dtype
     t = bias if bias.dtype in (dtype, torch.float32) else bias.to(torch.float32)
     if shape[3] != Sk:  # keys must be contiguous: materialise a broadcast key dimension
@@ -234,15 +261,16 @@ def prepare_bias(bias: torch.Tensor, B: int, H: int, Sq: int, Sk: int, dtype: to
         buf[..., :Sk] = t
         t = buf
         strides = [0 if t.shape[d] == 1 else t.stride(d) for d in range(3)] + [1]
-    return PreparedBias(t, _I64x4(*strides), DTYPE_CODES[t.dtype], shape, orig_dtype)
+    return PreparedBias(t, _I64x4(*strides), DTYPE_CODES[t.dtype], shape, orig_dtype, caller_shape)
 
 
 def reduce_dbias(dbias: torch.Tensor, pb: PreparedBias) -> torch.Tensor:
     """Sum the score gradient over the dimensions of the caller's bias that are
-    still broadcast (size 1 there, not here) and cast it to the bias's dtype."""
+    still broadcast (size 1 there, not here), cast it to the bias's dtype and
+    give it the caller's shape (a 2-D or 3-D bias gets a 2-D or 3-D gradient)."""
     dims = [d for d in range(4) if pb.shape[d] == 1 and dbias.shape[d] != 1]
     g = dbias.sum(dim=dims, keepdim=True) if dims else dbias
-    return g.to(pb.dtype)
+    return g.to(pb.dtype).reshape(pb.caller_shape)
 
 
 # The dropout keep mask a forward applied, bit-packed: int32 words (B*H*Sq,
@@ -291,7 +319,8 @@ def fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: 
         dropout_p: float = 0.0, seed: int = 0, offset: int = 0, want_max: bool = False, bias=None,
         keep_bits: Optional[torch.Tensor] = None):
     """Run ``fa_fwd``: returns (o, lse, max_vals or None).  Inputs (B, S, H, D);
-    ``bias`` a (B|1, H|1, Sq|1, Sk) tensor or a :class:`PreparedBias`;
+    ``bias`` a (B|1, H|1, Sq|1, Sk), (H, Sq, Sk) or (Sq, Sk) tensor or a
+    :class:`PreparedBias`;
     ``keep_bits`` (from :func:`alloc_keep_bits`, with dropout) receives the
     keep mask applied."""
     lib = load()

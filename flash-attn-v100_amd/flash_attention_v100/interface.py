@@ -7,8 +7,11 @@ enable_multi_gpu, enable_profiling, fallback_on_error, validate_inputs)`` on
 
 Single GPU only: the reference's Manager and its multi-GPU dispatch
 (``interface.py:25-196, 351-450``) are out of scope.  Validation checks
-metadata only (no full-tensor NaN scans, no host synchronisation; the
-reference's ``utils.py:227-254`` scans cost a sync each).
+metadata only by default (no full-tensor scans, no host synchronisation; the
+reference's ``utils.py:219-254`` scans cost a sync each); setting
+``config.DebugConfig.CHECK_NUMERICAL_STABILITY`` turns those scans on.  A bias
+may be (B|1, H|1, Sq|1, Sk), (H, Sq, Sk) or (Sq, Sk) (reference
+``utils.py:204-211``).
 
 Fallback (reference ``interface.py:331-348, 453-490``): with
 ``fallback_on_error=True`` a request the gfx950 kernels do not implement
@@ -30,6 +33,8 @@ from typing import Optional, Tuple, Union
 import torch
 
 from . import _lib
+from .config import DebugConfig
+from .utils import check_numerical_stability
 from .ops.attention import FlashAttentionV100Function, SUPPORTED_DTYPES, check_block_sizes
 
 _STRATEGIES = ("speed", "memory", "balanced", "adaptive")
@@ -72,11 +77,9 @@ def validate_inputs_enhanced(q, k, v, scale=None, bias=None, dropout_p=0.0):
     if q.device.type != "cuda":
         raise ValueError("Flash Attention requires GPU tensors (there is no CPU path)")
     if bias is not None:
-        if not isinstance(bias, torch.Tensor) or bias.dim() != 4:
-            raise ValueError("bias must be a 4-D tensor [batch|1, heads|1, seq_len_q|1, seq_len_k]")
-        if (bias.shape[3] != Sk or bias.shape[2] not in (1, Sq) or bias.shape[0] not in (1, B)
-                or bias.shape[1] not in (1, Hq)):
-            raise ValueError(f"bias shape {tuple(bias.shape)} is not broadcastable to {(B, Hq, Sq, Sk)}")
+        if not isinstance(bias, torch.Tensor):
+            raise TypeError("bias must be a torch.Tensor")
+        _lib.bias_as_4d(bias, B, Hq, Sq, Sk)  # the reference's shapes (utils.py:204-211), ValueError else
         if bias.device != q.device:
             raise ValueError(f"bias must be on {q.device}, got {bias.device}")
     if not (0.0 <= dropout_p < 1.0):
@@ -85,6 +88,8 @@ def validate_inputs_enhanced(q, k, v, scale=None, bias=None, dropout_p=0.0):
         scale = Dq ** -0.5
     if not (math.isfinite(scale) and scale > 0):
         raise ValueError(f"scale must be finite and positive, got {scale}")
+    if DebugConfig.CHECK_NUMERICAL_STABILITY:  # reference utils.py:142, 219-254 (opt-in here)
+        check_numerical_stability(q, k, v, bias)
     return q, k, v, scale
 
 

@@ -10,11 +10,17 @@ offset so the backward can reproduce the forward's mask (the reference never
 saved them, ``:209-227``); with dropout the forward also keeps the mask as bits
 for the backward when they fit ``_lib.KEEP_BITS_MAX_BYTES``.
 
-An additive ``bias`` of shape (B|1, H|1, Sq|1, Sk) is added to the scaled
-scores inside the kernels (reference ``kernels/forward_kernel.py:166-182``)
-and, when the bias requires grad, its real gradient dS (summed over broadcast
-dimensions) is returned in the bias slot; the reference returned zeros there
+An additive ``bias`` of shape (B|1, H|1, Sq|1, Sk), (H, Sq, Sk) or (Sq, Sk)
+(the shapes of the reference's validator, ``utils.py:204-211``) is added to
+the scaled scores inside the kernels (reference
+``kernels/forward_kernel.py:166-182``) and, when the bias requires grad, its
+real gradient dS (summed over broadcast dimensions, in the bias's own shape)
+is returned in the bias slot; the reference returned zeros there
 (``ops/attention.py:297-301``).
+
+With ``config.DebugConfig.VALIDATE_OUTPUTS`` set, inputs, outputs and
+gradients are checked for NaN / Inf as the reference does
+(``ops/attention.py:163-168, 203-206, 271-272, 304-310``); off by default.
 
 ``enable_gradient_checkpointing`` (or a :func:`gradient_checkpointing_mode`
 region) keeps only q, k, v and the LSE: the backward recomputes the output with
@@ -38,6 +44,8 @@ from typing import Any, Dict, Optional, Tuple
 import torch
 
 from .. import _lib
+from ..config import DebugConfig
+from ..utils import check_tensor_nan_inf
 
 SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
@@ -127,6 +135,9 @@ class EnhancedFlashAttentionV100Function(torch.autograd.Function):
         _check_kernel_inputs(q, k, v, dropout_p, bias)
         if scale is None:
             scale = q.shape[-1] ** -0.5
+        if DebugConfig.VALIDATE_OUTPUTS:  # reference ops/attention.py:163-168
+            for t, name in ((q, "query"), (k, "key"), (v, "value"), (bias, "bias")):
+                check_tensor_nan_inf(t, name)
         pb = _prepare_bias(bias, q, k)
         seed, offset = _lib.seed_offset(dropout_seed, dropout_offset) if dropout_p > 0 else (0, 0)
         recompute = bool(enable_gradient_checkpointing) or _CHECKPOINTING
@@ -134,11 +145,14 @@ class EnhancedFlashAttentionV100Function(torch.autograd.Function):
         if dropout_p > 0 and not recompute and any(ctx.needs_input_grad[:3] + ctx.needs_input_grad[6:7]):
             bits = _keep_bits_for(q, k)
         o, lse, _ = _lib.fwd(q, k, v, causal, scale, dropout_p, seed, offset, bias=pb, keep_bits=bits)
+        if DebugConfig.VALIDATE_OUTPUTS:  # reference ops/attention.py:203-206 (-inf LSE: a row with no visible key)
+            check_tensor_nan_inf(o, "output")
+            check_tensor_nan_inf(lse, "lse", allow_neg_inf=True)
         ctx.keep_bits = bits
         ctx.recompute_output = recompute
         kept = (q, k, v, lse) if recompute else (q, k, v, o, lse)
         ctx.save_for_backward(*kept, *(() if pb is None else (pb.tensor,)))
-        ctx.bias_meta = None if pb is None else (pb.strides, pb.dtype_code, pb.shape, pb.dtype)
+        ctx.bias_meta = None if pb is None else (pb.strides, pb.dtype_code, pb.shape, pb.dtype, pb.caller_shape)
         ctx.scale = scale
         ctx.causal = causal
         ctx.dropout_p = dropout_p
@@ -155,6 +169,8 @@ class EnhancedFlashAttentionV100Function(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_output: torch.Tensor, grad_softmax_lse: Optional[torch.Tensor] = None):
         # grad_softmax_lse is ignored, as in the reference (ops/attention.py:234-333)
+        if DebugConfig.VALIDATE_OUTPUTS:  # reference ops/attention.py:271-272
+            check_tensor_nan_inf(grad_output, "grad_output")
         saved = ctx.saved_tensors
         n = 4 if ctx.recompute_output else 5
         pb = None if ctx.bias_meta is None else _lib.PreparedBias(saved[n], *ctx.bias_meta)
@@ -175,6 +191,10 @@ class EnhancedFlashAttentionV100Function(torch.autograd.Function):
                          keep_bits=bits)
         ctx.keep_bits = None
         dq, dk, dv = grads[:3]
+        if DebugConfig.VALIDATE_OUTPUTS:  # reference ops/attention.py:304-310
+            for t, name in ((dq, "grad_q"), (dk, "grad_k"), (dv, "grad_v"), (grads[3] if want_dbias else None,
+                                                                            "grad_bias")):
+                check_tensor_nan_inf(t, name)
         return (
             dq if ctx.needs_input_grad[0] else None,
             dk if ctx.needs_input_grad[1] else None,

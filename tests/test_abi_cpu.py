@@ -423,8 +423,13 @@ def test_prepare_bias_layout():
     assert pb3.tensor.dtype == torch.float32
     with pytest.raises(ValueError):
         _lib.prepare_bias(torch.zeros(2, 2, 5, 16), 2, 3, 5, 16, torch.float16)
-    with pytest.raises(ValueError):
-        _lib.prepare_bias(torch.zeros(5, 16), 2, 3, 5, 16, torch.float16)
+    # 2-D (Sq, Sk) and 3-D (H, Sq, Sk) biases are the reference validator's
+    # shapes (utils.py:204-211); others of those ranks raise
+    assert _lib.prepare_bias(torch.zeros(5, 16), 2, 3, 5, 16, torch.float16).shape == (1, 1, 5, 16)
+    assert _lib.prepare_bias(torch.zeros(3, 5, 16), 2, 3, 5, 16, torch.float16).shape == (1, 3, 5, 16)
+    for bad in [(4, 16), (2, 5, 16), (5,)]:
+        with pytest.raises(ValueError):
+            _lib.prepare_bias(torch.zeros(*bad), 2, 3, 5, 16, torch.float16)
 
 
 def test_reduce_dbias_sums_broadcast_dims():

@@ -227,3 +227,45 @@ def test_gradient_checkpointing_recomputes_output(dtype, causal, p, with_bias, H
         o.backward(do)
     torch.cuda.synchronize()
     assert torch.equal(qq.grad, runs[0][1])
+
+
+def test_debug_validation_switch(monkeypatch):
+    """config.DebugConfig.VALIDATE_OUTPUTS (reference config.py:274,
+    ops/attention.py:163-168, 203-206, 271-272, 304-310): off by default, when
+    no check runs; on, a NaN in an input or in the incoming gradient raises
+    ValueError naming the tensor (with fallback_on_error the interface warns
+    and falls back, as the reference's does)."""
+    import warnings
+
+    import flash_attention_v100 as fa
+    from flash_attention_v100.config import DebugConfig
+    from flash_attention_v100.ops import attention as att
+    say("case: debug validation switch, (1, 64, 2, 64) bf16")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(1, 64, 2, 64, torch.bfloat16, seed=3))
+    calls = []
+    real = att.check_tensor_nan_inf
+    monkeypatch.setattr(att, "check_tensor_nan_inf", lambda t, name, **kw: (calls.append(name), real(t, name, **kw))[1])
+    qn = q.clone()
+    qn[0, 3, 1, 5] = float("nan")
+    o = fa.flash_attention_v100(qn, k, v, fallback_on_error=False)
+    torch.cuda.synchronize()
+    assert calls == [] and bool(torch.isnan(o).any())
+    monkeypatch.setattr(DebugConfig, "VALIDATE_OUTPUTS", True)
+    with pytest.raises(ValueError, match=r"^query contains 1 NaN values$"):
+        fa.flash_attention_v100(qn, k, v, fallback_on_error=False)
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        fa.flash_attention_v100(qn, k, v, fallback_on_error=True)
+    assert any("falling back" in str(x.message) for x in w)
+    calls.clear()
+    qg = q.clone().requires_grad_()
+    o = fa.flash_attention_v100(qg, k, v, causal=True, fallback_on_error=False)
+    o.backward(do)
+    assert calls == ["query", "key", "value", "bias", "output", "lse", "grad_output", "grad_q", "grad_k",
+                     "grad_v", "grad_bias"]
+    qg.grad = None
+    o = fa.flash_attention_v100(qg, k, v, causal=True, fallback_on_error=False)
+    dbad = do.clone()
+    dbad[0, 0, 0, 0] = float("inf")
+    with pytest.raises(ValueError, match=r"^grad_output contains 1 Inf values$"):
+        o.backward(dbad)

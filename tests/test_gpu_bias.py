@@ -474,3 +474,27 @@ def test_dbias_side_stream_from_two_threads():
         t.join(timeout=120)
     assert not any(t.is_alive() for t in threads), "a worker did not finish"
     assert not errors, errors
+
+
+@pytest.mark.parametrize("kind", ["SqSk", "HSqSk"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_bias_2d_3d_shapes(kind, causal):
+    """The reference validator's 2-D (Sq, Sk) position bias and 3-D (H, Sq, Sk)
+    per-head bias (utils.py:204-211) through the autograd entry point: read as
+    (1, 1, Sq, Sk) and (1, H, Sq, Sk), gradient returned in the caller's shape
+    (checked against the oracle's gradient of that 4-D view)."""
+    dt, B, S, H, D = torch.bfloat16, 2, 160, 4, 64
+    say(f"case: {kind} bias through flash_attention_v100, causal={causal}")
+    q, k, v, do = make_inputs(B, S, H, D, dt, seed=12)
+    shape = (S, S) if kind == "SqSk" else (H, S, S)
+    bias = make_bias(shape, dt)
+    view = bias.reshape((1, 1, S, S) if kind == "SqSk" else (1, H, S, S))
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    bd = bias.to(DEV).requires_grad_()
+    o, lse = fa.flash_attention_v100(qd, kd, vd, causal=causal, bias=bd, return_softmax_lse=True,
+                                     fallback_on_error=False)
+    o.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    assert bd.grad.shape == shape and bd.grad.dtype == dt
+    outs = (o.detach(), lse, qd.grad, kd.grad, vd.grad, bd.grad.reshape(view.shape))
+    check(q, k, v, do, causal, D ** -0.5, view, outs, label=f"{kind}-causal{causal}")

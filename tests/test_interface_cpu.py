@@ -168,3 +168,88 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(_lib.FlashAttentionExtensionError, match="build"):
         _lib.load(str(tmp_path / "nope.so"))
+
+
+# ---- bias shapes of the reference's validator (utils.py:204-211) ----
+
+def test_validation_accepts_reference_bias_shapes(monkeypatch):
+    B, S, H, D = 2, 8, 4, 64
+    q = _t(B, S, H, D)
+    monkeypatch.setattr(torch.Tensor, "device", property(lambda self: torch.device("cuda", 0)))
+    for shape in [(B, H, S, S), (1, H, S, S), (B, 1, S, S), (1, 1, S, S), (H, S, S), (S, S)]:
+        validate_inputs_enhanced(q, q, q, None, _t(*shape), 0.0)
+    for shape in [(B, S, S), (S, S + 1), (H, S, S + 1), (S,), (1, 1, 1, S, S)]:
+        with pytest.raises(ValueError, match="bias"):
+            validate_inputs_enhanced(q, q, q, None, _t(*shape), 0.0)
+    with pytest.raises(TypeError, match="bias"):
+        validate_inputs_enhanced(q, q, q, None, [[0.0]], 0.0)
+
+
+@pytest.mark.parametrize("shape,view", [((3, 5, 7), (1, 3, 5, 7)), ((5, 7), (1, 1, 5, 7)),
+                                        ((2, 1, 5, 7), (2, 1, 5, 7))])
+def test_prepare_bias_views_and_gradient_shape(shape, view):
+    B, H, Sq, Sk = 2, 3, 5, 7
+    g = torch.Generator().manual_seed(5)
+    bias = torch.randn(*shape, generator=g).to(torch.bfloat16)
+    pb = _lib.prepare_bias(bias, B, H, Sq, Sk, torch.bfloat16)
+    assert pb.shape == view and pb.caller_shape == shape and pb.dtype == torch.bfloat16
+    # the kernels read element (b, h, i, j) at the 4-D strides (zero on broadcast dims)
+    st = list(pb.strides)
+    seen = torch.as_strided(pb.tensor, (B, H, Sq, Sk), st, pb.tensor.storage_offset())
+    assert st[3] == 1 and torch.equal(seen, bias.reshape(view).expand(B, H, Sq, Sk))
+    # the score gradient (B, H, Sq, Sk) comes back summed and in the caller's shape
+    ds = torch.randn(B, H, Sq, Sk, generator=g)
+    want = ds.sum(dim=[d for d in range(4) if view[d] == 1], keepdim=True).reshape(shape).to(torch.bfloat16)
+    got = _lib.reduce_dbias(ds, pb)
+    assert got.shape == shape and torch.equal(got, want)
+
+
+# ---- opt-in NaN / Inf validation (reference config.py:274, ops/attention.py:163-168) ----
+
+def test_debug_switches_off_by_default():
+    from flash_attention_v100.config import DebugConfig
+    assert DebugConfig.VALIDATE_OUTPUTS is False and DebugConfig.CHECK_NUMERICAL_STABILITY is False
+    assert fa.DebugConfig is DebugConfig
+
+
+def test_check_tensor_nan_inf():
+    from flash_attention_v100.utils import check_tensor_nan_inf
+    x = torch.tensor([1.0, float("nan"), float("inf"), float("-inf"), float("nan")])
+    with pytest.raises(ValueError, match=r"^query contains 2 NaN values and 2 Inf values$"):
+        check_tensor_nan_inf(x, "query")
+    with pytest.raises(ValueError, match=r"^lse contains 2 NaN values and 1 Inf values$"):
+        check_tensor_nan_inf(x, "lse", allow_neg_inf=True)
+    ok = torch.tensor([0.0, -float("inf")])
+    assert check_tensor_nan_inf(ok, "lse", allow_neg_inf=True) is ok
+    with pytest.warns(UserWarning, match="Attempting to fix"):
+        fixed = check_tensor_nan_inf(x, "x", fix_issues=True)
+    assert torch.isfinite(fixed).all() and fixed[1] == 0 and fixed[0] == 1
+    assert check_tensor_nan_inf(None, "none") is None
+
+
+def test_check_numerical_stability():
+    from flash_attention_v100.utils import check_numerical_stability
+    a = torch.ones(2, 3)
+    check_numerical_stability(a, a, a)
+    with pytest.raises(ValueError, match="key tensor contains NaN values"):
+        check_numerical_stability(a, torch.full((2, 3), float("nan")), a)
+    with pytest.raises(ValueError, match="bias tensor contains Inf values"):
+        check_numerical_stability(a, a, a, torch.full((2,), float("inf")))
+    with pytest.warns(UserWarning, match="very large values"):
+        check_numerical_stability(a * 2e4, a, a)
+    with pytest.warns(UserWarning, match="very small values"):
+        check_numerical_stability(a, a, (a * 1e-8).to(torch.bfloat16))
+
+
+def test_numerical_scan_only_when_switched_on(monkeypatch):
+    from flash_attention_v100 import interface
+    from flash_attention_v100.config import DebugConfig
+    q = _t(2, 8, 4, 64)
+    monkeypatch.setattr(torch.Tensor, "device", property(lambda self: torch.device("cuda", 0)))
+    calls = []
+    monkeypatch.setattr(interface, "check_numerical_stability", lambda *a: calls.append(a))
+    validate_inputs_enhanced(q, q, q)
+    assert calls == []
+    monkeypatch.setattr(DebugConfig, "CHECK_NUMERICAL_STABILITY", True)
+    validate_inputs_enhanced(q, q, q)
+    assert len(calls) == 1
