@@ -1,12 +1,23 @@
 // Host side of the C ABI declared in include/fa_abi.h: argument validation
 // (pure host code, no HIP call before it passes) and dispatch to the dtype
-// launchers.  Stateless and re-entrant; launches on the caller's stream and
-// never synchronises.
+// launchers.  Launches on the caller's stream and never synchronises.
+// Library state, all of it per GPU and created lazily:
+//  * a 32 MiB static __device__ scratch (fa_bwd_static's workspace), reserved
+//    in every process that loads the library, and its address (looked up once
+//    under g_scratch_mu);
+//  * only when the environment sets FA_DBIAS_SIDE_STREAM=1: one side stream
+//    and two events, on which the whole backward writes the zero tails of a
+//    causal bias gradient beside the dK/dV pass; enqueues that use it are
+//    serialised by g_side_mu, and it is never used while the caller's stream
+//    (or the side stream) is being captured into a graph.
+// Without that variable every call is stateless apart from the scratch, and
+// re-entrant from any number of threads and streams.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
 #include <mutex>
 
 #include "fa_abi.h"
@@ -74,9 +85,10 @@ void* static_scratch(hipStream_t s) {
 }
 
 // A library-owned stream per GPU (default priority, non-blocking) with a fork
-// and a join event, for work of fa_bwd that runs beside the caller's stream:
-// created on first use with that GPU current; nullptr if any HIP call fails.
-// The caller holds g_side_mu from the fork to its join.
+// and a join event, for work of fa_bwd that runs beside the caller's stream
+// (opt-in, FA_DBIAS_SIDE_STREAM=1): created on first use with that GPU
+// current; nullptr if any HIP call fails.  The caller holds g_side_mu from the
+// fork to its join.
 struct SideStream {
     hipStream_t s = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
@@ -119,6 +131,23 @@ SideStream* side_stream(int dev) {
     ss.fork = ef;
     ss.join = ej;
     return &ss;
+}
+
+// FA_DBIAS_SIDE_STREAM=1 in the environment (read at each call)
+bool side_stream_wanted() {
+    const char* v = std::getenv("FA_DBIAS_SIDE_STREAM");
+    return v != nullptr && v[0] == '1' && v[1] == '\0';
+}
+
+// whether a stream is being captured into a graph (true on a query error too:
+// then the side stream is not used)
+bool capturing(hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return true;
+    }
+    return st != hipStreamCaptureStatusNone;
 }
 
 int elem_size(int32_t dtype) { return dtype == FA_DTYPE_F32 ? 4 : 2; }
@@ -567,21 +596,29 @@ int32_t bwd_run(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int32_t 
     hipStream_t s = (hipStream_t)stream;
     if (a->bias) {
         // The zero tails of a causal gradient written in place (2.15 GB at
-        // B=4, H=32, S=4096 bf16) are pure HBM writes: in the whole backward
-        // they run on the side stream while the compute-bound dK/dV pass runs
-        // on the caller's, which waits for them (join) before it returns.
+        // B=4, H=32, S=4096 bf16) are pure HBM writes.  By default the dQ pass
+        // writes them on the caller's stream (dbias_zero_fill 2).  With
+        // FA_DBIAS_SIDE_STREAM=1 the whole backward writes them on the side
+        // stream while the compute-bound dK/dV pass runs on the caller's,
+        // which waits for them (join) before the call returns -- unless either
+        // stream is being captured (a stream that joined a capture stays in it
+        // until the capture ends, so other calls' work would land in the
+        // graph): then the dQ pass writes them as by default.
         std::unique_lock<std::mutex> side_lock(g_side_mu, std::defer_lock);
         SideStream* ss = nullptr;
-        if (side && stage < 0 && causal && p.dbias_zero_fill == 2) {
+        bool joined = false;  // the side stream waits on this call's fork
+        if (side && stage < 0 && causal && p.dbias_zero_fill == 2 && side_stream_wanted() && !capturing(s)) {
             side_lock.lock();
             ss = side_stream(stream_device(s));
-            if (ss) {
+            if (ss && !capturing(ss->s)) {
                 hipError_t e = hipEventRecord(ss->fork, s);
                 if (e == hipSuccess) e = hipStreamWaitEvent(ss->s, ss->fork, 0);
-                if (e == hipSuccess) e = fa::launch_dbias_zero_tails(p, ss->s);
-                if (e == hipSuccess) e = hipEventRecord(ss->join, ss->s);
-                if (e != hipSuccess) return status_of(e);
-                p.dbias_zero_fill = 3;
+                if (e == hipSuccess) {
+                    joined = true;
+                    e = fa::launch_dbias_zero_tails(p, ss->s);
+                    if (e == hipSuccess) p.dbias_zero_fill = 3;  // written there; the dQ pass skips them
+                }
+                (void)hipGetLastError();  // a failed fork falls back to the dQ pass's tails
             }
         }
         const bool b32 = a->bias_dtype == FA_DTYPE_F32;
@@ -600,10 +637,12 @@ int32_t bwd_run(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int32_t 
         }
         // the summed gradient follows the dK/dV stage (stream order)
         if (e == hipSuccess && reduce_db && (stage < 0 || stage == 1)) e = fa::launch_dbias_reduce(rp, s);
-        // join (also after a failed launch: nothing of this call may outlive it
-        // on the side stream unordered with the caller's stream)
-        if (p.dbias_zero_fill == 3) {
-            const hipError_t ej = hipStreamWaitEvent(s, ss->join, 0);
+        // join, whenever the side stream waited on the fork (also after a
+        // failed launch: nothing of this call may outlive it on the side
+        // stream unordered with the caller's stream)
+        if (joined) {
+            hipError_t ej = hipEventRecord(ss->join, ss->s);
+            if (ej == hipSuccess) ej = hipStreamWaitEvent(s, ss->join, 0);
             if (e == hipSuccess) e = ej;
         }
         return status_of(e);

@@ -622,6 +622,10 @@ __global__ __launch_bounds__(576, 1) void fwd_pp_kernel(const FwdParams p) {
         vd.init(p.v_ss, lane, 0);
         constexpr int NKI = decltype(kd)::NI, NVI = decltype(vd)::NI;
         static_assert(2 * NKI + NVI <= 63, "vmcnt range");
+        // keys past the workgroup's last tile are never read: copies of tiles
+        // from n_tiles on read nothing (empty range, zeros land) but are still
+        // issued, so the vmcnt counts below stay exact
+        const int k_lim = min(p.Sk, n_tiles * BN);
         lds_barrier();
         for (int r = 0; r <= n_tiles; ++r) {
             const int j = r + 3;
@@ -629,11 +633,11 @@ __global__ __launch_bounds__(576, 1) void fwd_pp_kernel(const FwdParams p) {
             // round r-2's K(r+1), V(r) have landed (only round r-1's copies may
             // be in flight): the next barrier publishes them for M(r+1)
             wait_vmem_below<NKI + NVI>();
-            kd.load_untracked(kbase + (int64_t)(j * BN) * p.k_ss, p.k_ss, p.Sk - j * BN,
+            kd.load_untracked(kbase + (int64_t)(j * BN) * p.k_ss, p.k_ss, k_lim - j * BN,
                               Ks0 + (j % NSLOT) * C::KTILE, lane);
             barrier_no_fence();
             wait_vmem_below<63 - NVI>();
-            vd.load_untracked(vbase + (int64_t)((j - 1) * BN) * p.v_ss, p.v_ss, p.Sk - (j - 1) * BN,
+            vd.load_untracked(vbase + (int64_t)((j - 1) * BN) * p.v_ss, p.v_ss, k_lim - (j - 1) * BN,
                               Vs0 + ((j - 1) % NSLOT) * C::VTILE, lane);
         }
         barrier_no_fence();  // the one waves 0-3 pass after their last round

@@ -18,7 +18,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfa_gfx950.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 HEAD_DIMS = (32, 64, 128)  # compiled into the kernels for every dtype, with or without a bias
 WIDE_HEAD_DIM = 256        # compiled for fp16 / bf16 inputs without a bias
 MAX_HEAD_DIM = WIDE_HEAD_DIM

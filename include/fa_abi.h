@@ -6,6 +6,15 @@
  * allocates).  Work is enqueued on the caller's HIP stream; no call
  * synchronises the host.
  *
+ * State held by the library (per GPU, created lazily): fa_bwd_static's
+ * device scratch (FA_BWD_STATIC_SCRATCH_BYTES of static __device__ memory,
+ * reserved in every process that loads the library) and its looked-up
+ * address; and, only when the environment sets FA_DBIAS_SIDE_STREAM=1, one
+ * stream and two events on which fa_bwd writes the zero tails of a causal
+ * bias gradient (see fa_bwd).  Every entry point may be called from any
+ * number of host threads on any streams at once, except that fa_bwd_static
+ * calls on one GPU share its scratch (see there).
+ *
  * Layout: q, o, dq, dout are (B, Sq, H, D); k, v, dk, dv are (B, Sk, Hkv, D);
  * strides are in ELEMENTS in the order (b, s, h, d); the d stride must be 1,
  * base pointers 16-byte aligned and the b/s/h strides multiples of 16 bytes.
@@ -39,7 +48,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 2
+#define FA_ABI_VERSION 3
 
 /* element types */
 #define FA_DTYPE_F16 0
@@ -194,12 +203,15 @@ int32_t fa_bwd_check(const fa_bwd_args* args, size_t workspace_bytes);
  * (launch at :279-316).  workspace: >= fa_bwd_workspace_size bytes,
  * 256-byte aligned device memory.  Stream-ordered on hip_stream.  With a
  * causal bias gradient written in place (16-bit inputs, dS read back by the
- * dQ pass), the zeros above each 128-query tile are written by a small kernel
- * on a stream the library owns (one per GPU, default priority, created on
- * first use), forked from hip_stream at entry and joined back to it before
- * return, so that they overlap the dK/dV pass; callers see the same ordering
- * as for any single-stream call.  fa_bwd_stage with stage -1 does the same;
- * its single stages and fa_bwd_static write them on hip_stream. */
+ * dQ pass), the zeros above each 128-query tile are written by the dQ pass on
+ * hip_stream.  Opt-in (environment FA_DBIAS_SIDE_STREAM=1, read at each
+ * call): a small kernel writes them instead on a stream the library owns (one
+ * per GPU, default priority, created on first use), forked from hip_stream at
+ * entry and joined back to it before return, so that they overlap the dK/dV
+ * pass; callers see the same ordering as for any single-stream call.  The
+ * side stream is not used while hip_stream (or the side stream) is being
+ * captured into a graph, nor by fa_bwd_stage's single stages or by
+ * fa_bwd_static; host-side enqueues that use it are serialised by a mutex. */
 int32_t fa_bwd(const fa_bwd_args* args, void* workspace, size_t workspace_bytes, void* hip_stream);
 
 /* One stage of fa_bwd: 0 = delta pre-pass (writes the workspace), 1 = dK/dV,
@@ -209,6 +221,8 @@ int32_t fa_bwd(const fa_bwd_args* args, void* workspace, size_t workspace_bytes,
  * dS, below).  Without a bias gradient, stages 1 and 2 only read the
  * workspace and are independent of each other, so after stage 0 a caller may
  * run them on two streams; stage 1 after stage 3 gives the same results.
+ * (Since ABI version 3: in version 2 stages 1 and 2 were independent after
+ * stage 0 in every case.)
  * With one (dbias non-NULL) and 16-bit inputs, stage 1 writes dS (into dbias,
  * or into the workspace for a gradient summed over broadcast dimensions) and
  * stage 2 computes dQ from it: stage 2 must follow stage 1, and stage 3 is

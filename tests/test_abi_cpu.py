@@ -26,7 +26,7 @@ def declared_functions():
 
 def test_library_loads_and_version():
     lib = _lib.load()
-    assert lib.fa_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.fa_abi_version() == _lib.ABI_VERSION == 3
 
 
 def test_exports_every_declared_function():

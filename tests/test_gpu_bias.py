@@ -379,13 +379,19 @@ def test_bias_staged_forward(case):
         assert_parity(res, dt, f"staged head {hh}")
 
 
-def test_dbias_zero_tails_beside_dkdv_equal_staged():
+@pytest.mark.parametrize("side", [False, True])
+def test_dbias_zero_tails_beside_dkdv_equal_staged(side, monkeypatch):
     """The whole backward with a causal bias gradient written in place writes
-    the gradient's zero row tails on the library's side stream, beside the
-    dK/dV pass, joined back to the caller's stream; run stage by stage the dQ
-    pass writes them.  Both must give the same bits, every element written,
-    from a non-default stream, on two calls in a row (the second smaller)."""
+    the gradient's zero row tails in its dQ pass, or (FA_DBIAS_SIDE_STREAM=1)
+    on the library's side stream, beside the dK/dV pass, joined back to the
+    caller's stream; run stage by stage the dQ pass writes them.  All must give
+    the same bits, every element written, from a non-default stream, on two
+    calls in a row (the second smaller)."""
     import ctypes
+    if side:
+        monkeypatch.setenv("FA_DBIAS_SIDE_STREAM", "1")
+    else:
+        monkeypatch.delenv("FA_DBIAS_SIDE_STREAM", raising=False)
     lib = _lib.load()
     side = torch.cuda.Stream()
     for B, S, H, D, dt in ((2, 640, 2, 128, torch.bfloat16), (1, 384, 3, 64, torch.float16)):
@@ -424,13 +430,14 @@ def test_dbias_zero_tails_beside_dkdv_equal_staged():
         assert torch.equal(outs[0][3].tril(), outs[0][3])
 
 
-def test_dbias_side_stream_from_two_threads():
+def test_dbias_side_stream_from_two_threads(monkeypatch):
     """Two host threads, each on its own stream, run the whole backward with a
-    causal bias gradient (zero tails forked onto the library's one side
-    stream per GPU and joined back) several times at once; every result equals
-    the single-threaded one bit for bit."""
+    causal bias gradient (FA_DBIAS_SIDE_STREAM=1: zero tails forked onto the
+    library's one side stream per GPU and joined back) several times at once;
+    every result equals the single-threaded one bit for bit."""
     import ctypes
     import threading
+    monkeypatch.setenv("FA_DBIAS_SIDE_STREAM", "1")
     lib = _lib.load()
     say("case: dbias zero tails on the side stream from two threads")
     B, S, H, D, dt = 1, 512, 2, 64, torch.bfloat16
@@ -474,6 +481,59 @@ def test_dbias_side_stream_from_two_threads():
         t.join(timeout=120)
     assert not any(t.is_alive() for t in threads), "a worker did not finish"
     assert not errors, errors
+
+
+def test_dbias_side_stream_not_used_under_capture(monkeypatch):
+    """FA_DBIAS_SIDE_STREAM=1: a backward with a causal in-place bias gradient
+    captured into a graph writes its zero tails in the dQ pass (the side
+    stream would join the capture and pull other calls' work into it); an
+    eager backward on another stream while the capture is open still uses the
+    side stream, is not pulled into the graph and writes every element; the
+    capture ends cleanly, and every replay of the graph (with eager work and
+    synchronisations between them) equals the eager result bit for bit."""
+    import ctypes
+    monkeypatch.setenv("FA_DBIAS_SIDE_STREAM", "1")
+    lib = _lib.load()
+    B, S, H, D, dt = 1, 384, 2, 64, torch.bfloat16
+    say("case: dbias side stream and graph capture, (1, 384, 2, 64) bf16 causal")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, S, H, D, dt, seed=29))
+    bias = make_bias((B, H, S, S), dt, seed=29).to(DEV)
+    o, lse, _ = _lib.fwd(q, k, v, True, D ** -0.5, bias=bias)
+    pb = _lib.prepare_bias(bias, B, H, S, S, dt)
+    ref = _lib.bwd(q, k, v, o, do, lse, True, D ** -0.5, bias=pb, want_dbias=True)  # creates the side stream
+
+    def buffers():
+        dq, dk, dv = (torch.full_like(t, float("nan")) for t in (q, k, v))
+        db = torch.full((B, H, S, S), float("nan"), device=DEV, dtype=dt)
+        a = _lib.bwd_args(q, k, v, o, do, lse, dq, dk, dv, True, D ** -0.5, 0.0, 0, 0, pb, db)
+        ws = torch.empty(max(int(lib.fa_bwd_workspace_size(ctypes.byref(a))), 256), device=DEV, dtype=torch.uint8)
+        return a, ws, (dq, dk, dv, db)
+
+    cap_a, cap_ws, cap_out = buffers()
+    eag_a, eag_ws, eag_out = buffers()
+    torch.cuda.synchronize()
+    cap, eag = torch.cuda.Stream(), torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap, capture_error_mode="relaxed"):
+        code = lib.fa_bwd(ctypes.byref(cap_a), ctypes.c_void_p(cap_ws.data_ptr()), cap_ws.numel(),
+                          ctypes.c_void_p(cap.cuda_stream))
+        assert code == 0, _lib.strerror(code)
+        code = lib.fa_bwd(ctypes.byref(eag_a), ctypes.c_void_p(eag_ws.data_ptr()), eag_ws.numel(),
+                          ctypes.c_void_p(eag.cuda_stream))
+        assert code == 0, _lib.strerror(code)
+    eag.synchronize()
+    torch.cuda.synchronize()
+    assert all(torch.equal(x, y) for x, y in zip(eag_out, ref))
+    for rep in range(3):
+        for t in cap_out:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(x, y) for x, y in zip(cap_out, ref)), f"replay {rep}"
+        # eager work between replays
+        again = _lib.bwd(q, k, v, o, do, lse, True, D ** -0.5, bias=pb, want_dbias=True)
+        assert all(torch.equal(x, y) for x, y in zip(again, ref))
 
 
 @pytest.mark.parametrize("kind", ["SqSk", "HSqSk"])
