@@ -1715,37 +1715,52 @@ __global__ __launch_bounds__(512, 1) void dq_pp_kernel(const BwdParams p) {
     const int qi = qw0 + l32;
 
     // ---- Q, dO (and O) rows of this lane's query in registers (MFMA B operands) ----
+    // Branch-free buffer loads over the workgroup's rows [q0, min(Sq, q0 + BM)):
+    // rows past Sq read zeros (out of the descriptor's range).  All of the
+    // prologue's loads and copies are issued before its one wait (conditional
+    // loads made the compiler wait between them: several memory round trips
+    // per workgroup, exposed at one workgroup per CU).
     constexpr int QR = D / 16;
     const bool own_delta = p.dq_delta != 0;
+    const int qrows = min(p.Sq - q0, C::BM);  // >= 1: q0 < Sq
+    auto rows_rsrc = [&](const void* base, int64_t ss) FA_INLINE {
+        return slice_buffer((const T*)base + (int64_t)q0 * ss, ((qrows - 1) * (int)ss + D) * (int)sizeof(T));
+    };
+    const int rrow = 32 * blk + l32;  // this lane's row in the block
     uint4 qreg[QR], doreg[QR], oreg[QR];
     {
-        const T* qrow = (const T*)p.q + b * p.q_sb + (int64_t)qi * p.q_ss + h * p.q_sh;
-        const T* drow = (const T*)p.dout + b * p.do_sb + (int64_t)qi * p.do_ss + h * p.do_sh;
-        const T* orow = (const T*)p.o + b * p.o_sb + (int64_t)qi * p.o_ss + h * p.o_sh;
-        const bool ok = qi < p.Sq;
+        const __amdgpu_buffer_rsrc_t rq = rows_rsrc((const T*)p.q + b * p.q_sb + h * p.q_sh, p.q_ss);
+        const __amdgpu_buffer_rsrc_t rd = rows_rsrc((const T*)p.dout + b * p.do_sb + h * p.do_sh, p.do_ss);
 #pragma unroll
         for (int i = 0; i < QR; ++i) {
             const int d0 = 16 * i + 8 * hi;
-            qreg[i] = ok ? *reinterpret_cast<const uint4*>(qrow + d0) : make_uint4(0u, 0u, 0u, 0u);
-            doreg[i] = ok ? *reinterpret_cast<const uint4*>(drow + d0) : make_uint4(0u, 0u, 0u, 0u);
+            qreg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    rq, (rrow * (int)p.q_ss + d0) * (int)sizeof(T), 0, 0));
+            doreg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                     rd, (rrow * (int)p.do_ss + d0) * (int)sizeof(T), 0, 0));
         }
         if (own_delta) {
+            const __amdgpu_buffer_rsrc_t ro = rows_rsrc((const T*)p.o + b * p.o_sb + h * p.o_sh, p.o_ss);
 #pragma unroll
             for (int i = 0; i < QR; ++i)
-                oreg[i] = ok ? *reinterpret_cast<const uint4*>(orow + 16 * i + 8 * hi) : make_uint4(0u, 0u, 0u, 0u);
+                oreg[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        ro, (rrow * (int)p.o_ss + 16 * i + 8 * hi) * (int)sizeof(T), 0, 0));
         }
     }
     // the workspace rows hold sq_pad (Sq rounded up to 128) entries; the last
     // 256-query block may reach past them (its queries past Sq get P = 0)
     const bool in_ws = qi < p.sq_pad;
     const int64_t wi = ((int64_t)b * p.H + h) * p.ws_stride + qi;
-    float lse2 = INFINITY, del = 0.f, lse_in = 0.f;
-    if (own_delta)
-        lse_in = qi < p.Sq ? p.lse[((int64_t)b * p.H + h) * p.Sq + qi] : -INFINITY;
-    else if (in_ws) {
-        lse2 = p.lse2[wi];
-        del = p.delta[wi];
-    }
+    // the saved LSE (own_delta) or the workspace rows (after a delta pre-pass):
+    // both loaded without a branch, used after the tile copies are issued
+    // (rows past Sq / sq_pad read zeros and are replaced then)
+    const __amdgpu_buffer_rsrc_t rl = slice_buffer(p.lse + ((int64_t)b * p.H + h) * p.Sq, own_delta ? p.Sq * 4 : 0);
+    const __amdgpu_buffer_rsrc_t rw =
+        slice_buffer(p.lse2 + ((int64_t)b * p.H + h) * p.ws_stride, own_delta ? 0 : p.ws_stride * 4);
+    const float lse_raw = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, qi * 4, 0, 0));
+    const float ws_lse = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rw, qi * 4, 0, 0));
+    const float ws_del = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rw, (p.sq_pad + qi) * 4, 0, 0));
+    float lse2 = INFINITY, del = 0.f;
     const float c = p.scale_log2;
     f32x16 dq[D / 32];
 #pragma unroll
@@ -1916,14 +1931,20 @@ __global__ __launch_bounds__(512, 1) void dq_pp_kernel(const BwdParams p) {
 #pragma unroll
             for (int i = 0; i < st; ++i) cs[i] = cs[i] + cs[i + st];
         del = pair_sum(cs[0]);
+        const float lse_in = qi < p.Sq ? lse_raw : -INFINITY;
         lse2 = lse_in == -INFINITY ? INFINITY : lse_in * kLog2e;
-        if (hi == 0 && in_ws) {
-            p.lse2[wi] = lse2;
-            p.delta[wi] = del;
-        }
+    } else {
+        lse2 = in_ws ? ws_lse : INFINITY;
+        del = in_ws ? ws_del : 0.f;
     }
     wait_vmem();
     lds_barrier();
+    // the rows go to the workspace for the dK/dV pass (a later launch); issued
+    // after the barrier so that no wait of the prologue covers the stores
+    if (own_delta && hi == 0 && in_ws) {
+        p.lse2[wi] = lse2;
+        p.delta[wi] = del;
+    }
     if (grp == 1) barrier_no_fence();  // waves 4-7 run one phase behind
 
     // V phase of round r: this round's copies (tile r + 2 + grp; tiles 0-2 came
