@@ -371,12 +371,14 @@ def main():
     kernels = {"fwd_kernel": r["fwd_ms"]}
     kernels.update({names[st]: ms for st, ms in r["stage_ms"].items()})
     # the kernels each stage launches at this workload (the keys above name the stages)
-    stage_kernels = {"fwd_kernel": "fwd_pp_kernel (256-query ping-pong workgroups)", "dkdv_kernel": "dkdv_kernel"}
+    stage_kernels = {"fwd_kernel": "fwd_pp_kernel (256-query ping-pong workgroups)",
+                     "dkdv_kernel": "dkdv_pp_kernel (256-key ping-pong workgroups)"}
     if 3 in r["stage_ms"]:
-        stage_kernels["dq_kernel"] = "dq_kernel (computes and writes the delta rows; runs before dK/dV)"
+        stage_kernels["dq_kernel"] = ("dq_pp_kernel (256-query ping-pong workgroups; computes and writes the "
+                                      "delta rows; runs before dK/dV)")
     else:
         stage_kernels["delta_kernel"] = "delta_kernel"
-        stage_kernels["dq_kernel"] = "dq_kernel"
+        stage_kernels["dq_kernel"] = "dq_pp_kernel (256-query ping-pong workgroups)"
     if a.bias != "none":
         stage_kernels["fwd_kernel"] = "fwd_kernel (256-query workgroups, bias staged through LDS)"
         stage_kernels["dkdv_kernel"] = "dkdv8_kernel" + (" + dbias_reduce_kernel" if a.bias == "heads" and a.dbias else "")
