@@ -175,7 +175,10 @@ ALL_CONFIGS = [
     ("C4-causal", (1, 16384, 16, 128), "bfloat16", True, 0.0, True),
     ("C4-full", (1, 16384, 16, 128), "bfloat16", False, 0.0, True),
 ] + [(f"C5-D{d}-{'fp32' if dt == 'float32' else 'fp16'}", (8, 1000, 16, d), dt, True, 0.1, True)
-     for d in (32, 64, 128) for dt in ("float32", "float16")]
+     for d in (32, 64, 128) for dt in ("float32", "float16")] + [
+    # not a BASELINE config: head dim 256 (16-bit inputs, no bias) at a full-size shape
+    ("X-D256", (2, 4096, 16, 256), "bfloat16", True, 0.0, True),
+]
 
 
 def all_configs(n: int, cpu: bool, cpu_target_s: float = 3.0, only=None, warmup: int = 5):

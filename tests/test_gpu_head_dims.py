@@ -99,3 +99,19 @@ def test_head_dim_256_without_kernel_falls_back(what):
     s = s.masked_fill(torch.ones(S, S, dtype=torch.bool, device=DEV).triu(1), float("-inf"))
     ref = torch.matmul(torch.softmax(s, -1), v.float().transpose(1, 2)).transpose(1, 2)
     assert (out.float() - ref).abs().max().item() < (2e-2 if dt != torch.float32 else 1e-5)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_head_dim_256_full_size(causal):
+    # D = 256 at a full-size shape (4096 tokens, GQA 16 / 8 heads): O, LSE, dQ,
+    # dK, dV against the float64 oracle within the 2x envelope, as the
+    # BASELINE configs are checked
+    B, S, H, Hkv, D = 2, 4096, 16, 8, 256
+    print(f"case: D=256 full size ({B},{S},{H},{Hkv},{D}) bf16 causal={causal}", flush=True)
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, S, H, D, torch.bfloat16, Hkv=Hkv, seed=35))
+    scale = D ** -0.5
+    o, lse, _ = _lib.fwd(q, k, v, causal, scale)
+    dq, dk, dv = _lib.bwd(q, k, v, o, do, lse, causal, scale)
+    torch.cuda.synchronize()
+    res = compare(q, k, v, do, causal, scale, (o, lse, dq, dk, dv))
+    assert_parity(res, torch.bfloat16, f"D=256 full size causal={causal}")
