@@ -804,7 +804,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, cons
     // (m & 1) of tile m / 2, m = r + 3 (waves 0-3) or r + 4 (waves 4-7), tiles
     // 2 .. total - 1 (the prologue copied 0 and 1) -- then P, dS (zero where
     // the sub-step has no visible pair or there is no sub-step), then wait for
-    // this wave's copies of earlier rounds.
+    // this wave's copies of earlier rounds.  The slot schedule is modelled for
+    // every run length up to 100 tiles by tests/test_pp_schedule_cpu.py.
     Pos pc{0, 0, 0};  // tile m / 2 of the copies
     advance(pc);
     if (grp == 1) advance(pc);  // round 0: tile 1 (waves 0-3, nothing to copy) or 2 (waves 4-7)
@@ -1668,7 +1669,8 @@ __global__ __launch_bounds__(256 * KS, (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)) 
 // 4-7 V(r + 3) in round r (4 or 5 copy instructions each); a slot is refilled
 // only after both groups' M phases that read its previous tile, and a wave's
 // copies have landed before the barrier that opens the first M phase reading
-// them (the schedule of dkdv_pp_kernel's first version, checked on the host).
+// them (modelled for every run length up to 100 tiles by
+// tests/test_pp_schedule_cpu.py).
 // Per query the arithmetic is that of dq_kernel, in the same order (delta and
 // LSE * log2 e computed as there and written to the workspace rows for the
 // dK/dV pass), so dQ and the workspace rows are bit-identical to it.
