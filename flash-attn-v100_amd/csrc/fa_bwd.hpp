@@ -109,11 +109,19 @@ struct DkdvCfg {
     static_assert(BUF_BYTES % 16 == 0, "16-byte aligned buffers");
 };
 
-// TB: element type of the additive bias (T or float), void = no bias
-template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
+// TB: element type of the additive bias (T or float), void = no bias.
+// DA, DOFF: the kernel accumulates (and writes) only the dK / dV columns
+// [DOFF, DOFF + DA); S and dP still take every column of Q, K, V and dO.  Head
+// dim 256 runs it as two launches of 128 columns each: the dK / dV
+// accumulators of all 256 columns (256 floats a lane) beside the K and V rows
+// (128 registers) do not fit the 512 registers of a lane, and spilled them
+// (about 1.1 KiB of scratch a lane); the halves recompute S and dP, 1.5x the
+// products of one launch, with nothing spilled.
+template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB, int DA = D, int DOFF = 0>
 __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Elem<T>::kF32 && D == 128) && D <= 128 ? 2 : 1)) void dkdv_kernel(
     const BwdParams p, const int n_ktiles) {
     using C = DkdvCfg<T, D>;
+    static_assert(DA % 32 == 0 && DOFF % 32 == 0 && DOFF + DA <= D, "a range of whole 32-column blocks");
     constexpr bool BIAS = !std::is_void<TB>::value;
     using BT = typename std::conditional<BIAS, TB, T>::type;
     constexpr int BQ = C::BQ, RW = C::RW;
@@ -148,9 +156,9 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
     // no wait here: the K / V loads stay in flight while the first tile copy
     // is issued (the loop's first barrier waits for both)
 
-    f32x16 dk[D / 32], dv[D / 32];
+    f32x16 dk[DA / 32], dv[DA / 32];
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i) { dk[i] = f32x16{}; dv[i] = f32x16{}; }
+    for (int i = 0; i < DA / 32; ++i) { dk[i] = f32x16{}; dv[i] = f32x16{}; }
     const float c = p.scale_log2;
 
     // query tiles: causal needs queries >= k0 only; per query head of the
@@ -346,9 +354,9 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
             for (int t = 8 * H2; t < 8 * H2 + 8; ++t) {
                 const int qr = 8 * (t >> 2) + 4 * hi + (t & 3);
 #pragma unroll
-                for (int i = 0; i < D / 32; ++i) {
-                    dv[i] = mfma_f32(Ds[qr * RW + 32 * i + l32], pd[t], dv[i]);
-                    dk[i] = mfma_f32(Qs[qr * RW + 32 * i + l32], ds[t], dk[i]);
+                for (int i = 0; i < DA / 32; ++i) {
+                    dv[i] = mfma_f32(Ds[qr * RW + DOFF + 32 * i + l32], pd[t], dv[i]);
+                    dk[i] = mfma_f32(Qs[qr * RW + DOFF + 32 * i + l32], ds[t], dk[i]);
                 }
             }
         } else {
@@ -357,8 +365,8 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
             const int tcol = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
             constexpr int ks = H2;
 #pragma unroll
-                for (int i = 0; i < D / 32; ++i) {
-                    const int off = (16 * ks + trow) * RW + 32 * i + tcol;
+                for (int i = 0; i < DA / 32; ++i) {
+                    const int off = (16 * ks + trow) * RW + DOFF + 32 * i + tcol;
                     const s16x8 ad = cat4(lds_read_tr16(Ds + off), lds_read_tr16(Ds + off + 8 * RW));
                     const s16x8 aq = cat4(lds_read_tr16(Qs + off), lds_read_tr16(Qs + off + 8 * RW));
                     dv[i] = Elem<T>::mfma(ad, bp8[ks], dv[i]);
@@ -440,7 +448,7 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
     // ---- epilogue: stage dK^T, dV^T through LDS as rows, coalesced stores ----
     constexpr int OW = C::OW;
     constexpr int EPC = 16 / sizeof(T);
-    constexpr int CPR = D / EPC;
+    constexpr int CPR = DA / EPC;
     T* Os = (T*)smem + w * 32 * OW;
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
@@ -448,10 +456,10 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
         const f32x16* acc = pass == 0 ? dk : dv;
         const float mul = pass == 0 ? p.scale : (DROPOUT ? p.rp : 1.f);
 #pragma unroll
-        for (int i = 0; i < D / 32; ++i)
+        for (int i = 0; i < DA / 32; ++i)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int d = 32 * i + 8 * g + 4 * hi;
+                const int d = 32 * i + 8 * g + 4 * hi;  // column DOFF + d of dK / dV
                 if constexpr (C::F32) {
                     f32x4 v4;
 #pragma unroll
@@ -473,7 +481,7 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
             const int row = cidx / CPR, col = cidx % CPR;
             const int key = kw0 + row;
             if (key < p.Sk)
-                *reinterpret_cast<uint4*>(gbase + (int64_t)key * gss + col * EPC) =
+                *reinterpret_cast<uint4*>(gbase + (int64_t)key * gss + DOFF + col * EPC) =
                     *reinterpret_cast<const uint4*>(Os + row * OW + col * EPC);
         }
     }
@@ -2303,8 +2311,18 @@ hipError_t launch_bwd_t(const BwdParams& p0, int stage, hipStream_t s) {
                 done = true;
             }
         }
-        if (!done && nb > 0)
-            hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, DROPOUT, TB>), dim3((unsigned)nb), dim3(C::NT), 0, s, p, nk);
+        if constexpr (D == 256) {
+            // two launches of 128 dK / dV columns each (see dkdv_kernel)
+            if (!done && nb > 0) {
+                hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, DROPOUT, TB, 128, 0>), dim3((unsigned)nb), dim3(C::NT), 0, s,
+                                   p, nk);
+                hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, DROPOUT, TB, 128, 128>), dim3((unsigned)nb), dim3(C::NT), 0,
+                                   s, p, nk);
+            }
+        } else {
+            if (!done && nb > 0)
+                hipLaunchKernelGGL((dkdv_kernel<T, D, CAUSAL, DROPOUT, TB>), dim3((unsigned)nb), dim3(C::NT), 0, s, p, nk);
+        }
     }
     if (stage < 0 || stage == 2) {
         using C = DqCfg<T, D>;
