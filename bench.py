@@ -48,6 +48,11 @@ B, S, H, D = 4, 4096, 32, 128
 CAUSAL = True
 
 
+def _sig4(x: float) -> float:
+    """Four significant digits (a fixed number of decimals rounds a small CPU sample to 0)."""
+    return float(f"{x:.4g}")
+
+
 def f_fwd(b=B, h=H, s=S, d=D, causal=CAUSAL):
     return 4.0 * b * h * s * s * d * (0.5 if causal else 1.0)
 
@@ -159,7 +164,7 @@ def cpu_baseline(target_s: float = 12.0, bias_kind: str = "none"):
     times = [run(h) for _ in range(2)]
     t = min(times)
     flop = 3.5 * f_fwd(b=1, h=h)
-    return {"value": round(flop / t / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+    return {"value": _sig4(flop / t / 1e12), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": f"fwd+bwd of B=1, H={h} of the workload (S=4096, D=128, causal"
                       f"{'' if bias_kind == 'none' else ', additive bias with its gradient'}) in fp32 via "
@@ -289,7 +294,7 @@ def _cpu_sample(s, h_max, d, causal, p, with_bwd, target_s):
     h = int(max(1, min(h_max, target_s / max(t1, 1e-3))))
     t = min(run(h) for _ in range(2))
     flop = f_fwd(1, h, s, d, causal) * (3.5 if with_bwd else 1.0)
-    return {"value": round(flop / t / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+    return {"value": _sig4(flop / t / 1e12), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port", "sample": f"B=1, H={h} in fp32 via oracle.attention; best of 2 runs, {t:.2f} s each"}
 
 
