@@ -586,20 +586,16 @@ __global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, cons
     const int qt_end = (p.Sq + BQ - 1) / BQ;
     const int nq = qt_end > qt_begin ? qt_end - qt_begin : 0;
     const int total = nq * p.group;  // tiles; rounds = 2 * total
-    // position of a tile in the run (head in group, tile in the head's run,
-    // LDS slot), advanced one tile at a time: no integer division in the loop
+    // position of a round's tile in the run (tile in the head's run, LDS
+    // slot), advanced one tile at a time: no integer division in the loop
     struct Pos {
-        int h, i, s;
+        int i, s;
     };
     auto advance = [&](Pos& t) FA_INLINE {
-        if (++t.i == nq) {
-            t.i = 0;
-            ++t.h;
-        }
+        if (++t.i == nq) t.i = 0;
         if (++t.s == C::NSLOT) t.s = 0;
     };
     auto pos_q0 = [&](const Pos& t) FA_INLINE { return (qt_end - 1 - t.i) * BQ; };
-    auto pos_head = [&](const Pos& t) FA_INLINE { return hk * p.group + t.h; };
     auto slot = [&](int s) FA_INLINE -> char* { return smem + s * C::SLOT_BYTES; };
     // this wave's sub-step (first query qs0): any visible (query, key) pair,
     // and any masked one
@@ -640,22 +636,58 @@ __global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, cons
             const int row = cidx / C::CW, col = cidx % C::CW;
             coff[hf][n] = col < D / C::EPC ? (row * (int)css + col * C::EPC) * (int)sizeof(T) : kOffNowhere;
         }
-    // half hf of tile t (slot): the wave's items 8 n + 4 hf + w4 of the group's 20
-    auto issue = [&](const Pos& t, int hf) FA_INLINE {
-        const int hh = pos_head(t), qb0 = pos_q0(t);
-        char* sp = slot(t.s);
-        // the tile's rows [0, min(Sq - qb0, BQ)); rows past it land as zeros
-        const int nv = q_rows - qb0;
-        const uint32_t bytes = nv >= BQ ? full_bytes : (uint32_t)(((nv - 1) * (int)css + D) * (int)sizeof(T));
-        const uint64_t src = cbase + (uint64_t)(int64_t)qb0 * crow + (uint64_t)hh * chead;
+    // The copy position: the current tile's sources and ranges (rows and the
+    // workspace row) and LDS slot, advanced one tile at a time by additions:
+    // within a head's run the tiles step down by BQ rows and only the first
+    // tile of a run (the last rows) can be partial.
+    struct Cp {
+        uint64_t src, hsrc, wsrc, hwsrc;
+        uint32_t bytes, wbytes, lds;
+        int i;
+    };
+    const int qb0_first = (qt_end - 1) * BQ;
+    const uint32_t bytes_first = opaque32(
+        q_rows - qb0_first >= BQ ? full_bytes : (uint32_t)(((q_rows - qb0_first - 1) * (int)css + D) * (int)sizeof(T)));
+    const uint32_t wbytes_first = opaque32(wrow_bytes - 4u * (uint32_t)qb0_first);
+    const uint64_t dsrc = opaque64((uint64_t)BQ * crow);
+    const uint32_t lds_first = __builtin_amdgcn_readfirstlane(lds_addr(smem + grp * C::QALLOC));
+    const uint32_t lds_wrap = lds_first + C::NSLOT * C::SLOT_BYTES;
+    const uint32_t lse_off = (uint32_t)((2 - grp) * C::QALLOC + grp * 4 * BQ);  // the workspace row's LDS offset
+    Cp c0;
+    c0.hsrc = opaque64(cbase + (uint64_t)(int64_t)qb0_first * crow + (uint64_t)(hk * p.group) * chead);
+    c0.src = c0.hsrc;
+    c0.hwsrc = opaque64(wbase + (uint64_t)(hk * p.group) * wrow_bytes + 4u * (uint32_t)qb0_first);
+    c0.wsrc = c0.hwsrc;
+    c0.bytes = bytes_first;
+    c0.wbytes = wbytes_first;
+    c0.lds = lds_first;
+    c0.i = 0;
+    auto advance_cp = [&](Cp& t) FA_INLINE {
+        if (++t.i == nq) {
+            t.i = 0;
+            t.hsrc += chead;
+            t.hwsrc += wrow_bytes;
+            t.src = t.hsrc;
+            t.wsrc = t.hwsrc;
+            t.bytes = bytes_first;
+            t.wbytes = wbytes_first;
+        } else {
+            t.src -= dsrc;
+            t.wsrc -= 4u * BQ;
+            t.bytes = full_bytes;
+            t.wbytes += 4u * BQ;
+        }
+        t.lds += C::SLOT_BYTES;
+        if (t.lds == lds_wrap) t.lds = lds_first;
+    };
+    // half hf of the tile at t: the wave's items 8 n + 4 hf + w4 of the group's 20
+    auto issue = [&](const Cp& t, int hf) FA_INLINE {
         u32x4 rs;
-        rs[0] = (uint32_t)src;
-        rs[1] = (uint32_t)(src >> 32) & 0xFFFFu;
-        rs[2] = bytes;
+        rs[0] = (uint32_t)t.src;
+        rs[1] = (uint32_t)(t.src >> 32) & 0xFFFFu;
+        rs[2] = t.bytes;
         rs[3] = 0x00020000u;
-        // (scalar: M0 takes the LDS address; computed with vector ops, it
-        // would not be accepted as the asm's scalar operand)
-        const uint32_t l0 = __builtin_amdgcn_readfirstlane(lds_addr(sp + grp * C::QALLOC));
+        const uint32_t l0 = t.lds;
         auto items = [&](auto hf_tag) FA_INLINE {
             constexpr int HF = decltype(hf_tag)::value;
 #pragma unroll
@@ -664,14 +696,12 @@ __global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, cons
                 if (g < C::NI) {
                     dma_load16_untracked(rs, __builtin_amdgcn_readfirstlane(l0 + 1024 * g), coff[HF][n]);
                 } else if (g == C::NI) {  // the LSE (waves 0-3) or delta (waves 4-7) row, one dword per lane
-                    const uint64_t wsrc = wbase + (uint64_t)hh * wrow_bytes + 4u * (uint32_t)qb0;  // qb0 + BQ <= sq_pad
-                    u32x4 ws;
-                    ws[0] = (uint32_t)wsrc;
-                    ws[1] = (uint32_t)(wsrc >> 32) & 0xFFFFu;
-                    ws[2] = wrow_bytes - 4u * (uint32_t)qb0;
+                    u32x4 ws;  // (rows qb0 .. qb0 + BQ <= sq_pad)
+                    ws[0] = (uint32_t)t.wsrc;
+                    ws[1] = (uint32_t)(t.wsrc >> 32) & 0xFFFFu;
+                    ws[2] = t.wbytes;
                     ws[3] = 0x00020000u;
-                    dma_load4_untracked(ws, __builtin_amdgcn_readfirstlane(lds_addr(sp + 2 * C::QALLOC + grp * 4 * BQ)),
-                                        woff);
+                    dma_load4_untracked(ws, __builtin_amdgcn_readfirstlane(l0 + lse_off), woff);
                 }
             }
         };
@@ -795,13 +825,13 @@ __global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, cons
 
     // prologue: tiles 0 and 1, every wave its group's 6 instructions of each
     {
-        Pos t{0, 0, 0};
+        Cp t = c0;
         for (int j = 0; j < 2; ++j) {
             if (j < total) {
                 issue(t, 0);
                 issue(t, 1);
             }
-            advance(t);
+            advance_cp(t);
         }
     }
     wait_vmem();
@@ -814,15 +844,15 @@ __global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, cons
     // the sub-step has no visible pair or there is no sub-step), then wait for
     // this wave's copies of earlier rounds.  The slot schedule is modelled for
     // every run length up to 100 tiles by tests/test_pp_schedule_cpu.py.
-    Pos pc{0, 0, 0};  // tile m / 2 of the copies
-    advance(pc);
-    if (grp == 1) advance(pc);  // round 0: tile 1 (waves 0-3, nothing to copy) or 2 (waves 4-7)
+    Cp pc = c0;  // tile m / 2 of the copies
+    advance_cp(pc);
+    if (grp == 1) advance_cp(pc);  // round 0: tile 1 (waves 0-3, nothing to copy) or 2 (waves 4-7)
     auto vround = [&](int r, const Pos& pr, int st, bool act) FA_INLINE {
         const int m = r + 3 + grp;
         const int j = m >> 1;
         const bool cp = j >= 2 && j < total;
         if (cp) issue(pc, m & 1);
-        if (m & 1) advance(pc);
+        if (m & 1) advance_cp(pc);
         if (act) {
             const int qs0 = pos_q0(pr) + 32 * st;
             vphase(pr.s, st, qs0, masked(qs0));
@@ -846,7 +876,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, cons
     // round 2 total (no sub-step) are not used.  Idle products cost no time,
     // as the workgroup's waves run in lock step.
     if (total > 0) {
-        Pos pr{0, 0, 0};  // tile of round r
+        Pos pr{0, 0};  // tile of round r
         sched_fence();
         mphase(0, 0, 0, 0, FF{}, TT{});
         sched_fence();
@@ -1790,6 +1820,10 @@ __global__ __launch_bounds__(512, 1) void dq_pp_kernel(const BwdParams p) {
         asm volatile("" : "+s"(x));
         return x;
     };
+    auto opaque32 = [](uint32_t x) FA_INLINE {
+        asm volatile("" : "+s"(x));
+        return x;
+    };
     const int64_t css = grp == 0 ? p.k_ss : p.v_ss;
     const uint64_t cbase = opaque64((uint64_t)(uintptr_t)(grp == 0 ? (const T*)p.k + b * p.k_sb + hk * p.k_sh
                                                                    : (const T*)p.v + b * p.v_sb + hk * p.v_sh));
@@ -1806,23 +1840,34 @@ __global__ __launch_bounds__(512, 1) void dq_pp_kernel(const BwdParams p) {
     }
     auto slot = [&](int r) FA_INLINE -> char* { return smem + (r & (NSLOT - 1)) * C::SLOT_BYTES; };
     static_assert(NSLOT == 4, "slot index by mask");
-    auto issue = [&](int j) FA_INLINE {
-        const int k0 = j * BN;
-        const int nv = p.Sk - k0;  // > 0: j < n_tiles
-        const uint32_t bytes = nv >= BN ? full_bytes : (uint32_t)(((nv - 1) * (int)css + D) * (int)sizeof(T));
-        const uint64_t src = cbase + (uint64_t)(int64_t)k0 * crow;
+    // tile j < n_tiles at source src, LDS address l0: the keys [j BN, min(Sk, j BN + BN)),
+    // rows past Sk land as zeros (only the last tile can be partial)
+    const uint32_t last_bytes = opaque32(
+        p.Sk - (n_tiles - 1) * BN >= BN ? full_bytes
+                                        : (uint32_t)(((p.Sk - (n_tiles - 1) * BN - 1) * (int)css + D) * (int)sizeof(T)));
+    auto issue_at = [&](int j, uint64_t src, uint32_t l0) FA_INLINE {
         u32x4 rs;
         rs[0] = (uint32_t)src;
         rs[1] = (uint32_t)(src >> 32) & 0xFFFFu;
-        rs[2] = bytes;
+        rs[2] = j == n_tiles - 1 ? last_bytes : full_bytes;
         rs[3] = 0x00020000u;
-        const uint32_t l0 = __builtin_amdgcn_readfirstlane(lds_addr(slot(j) + grp * C::KALLOC));
 #pragma unroll
         for (int t = 0; t < C::PER; ++t) {
             const int g = w4 + 4 * t;  // wave-uniform
             if (g < C::NI) dma_load16_untracked(rs, __builtin_amdgcn_readfirstlane(l0 + 1024 * g), coff[t]);
         }
     };
+    auto issue = [&](int j) FA_INLINE {
+        issue_at(j, cbase + (uint64_t)(int64_t)(j * BN) * crow,
+                 __builtin_amdgcn_readfirstlane(lds_addr(slot(j) + grp * C::KALLOC)));
+    };
+    // the rounds' copy cursor (tile r + 2 + grp): source and LDS slot advanced
+    // by additions, no multiplication in the loop
+    const uint64_t dsrc = opaque64((uint64_t)BN * crow);
+    const uint32_t lds_first = __builtin_amdgcn_readfirstlane(lds_addr(smem + grp * C::KALLOC));
+    const uint32_t lds_wrap = lds_first + NSLOT * C::SLOT_BYTES;
+    uint64_t kc_src = opaque64(cbase + (uint64_t)(2 + grp) * dsrc);
+    uint32_t kc_lds = lds_first + (uint32_t)(((2 + grp) & (NSLOT - 1)) * C::SLOT_BYTES);
 
     // ---- M phase: dQ^T of the previous tile, then S^T / dP^T of this one ----
     // dQ step t (t = ks (D / 32) + i, ks = 16-key step of the 64): K^T of keys
@@ -1963,7 +2008,10 @@ __global__ __launch_bounds__(512, 1) void dq_pp_kernel(const BwdParams p) {
     auto vround = [&](int r) FA_INLINE {
         const int j = r + 2 + grp;
         const bool cp = j >= 3 && j < n_tiles;
-        if (cp) issue(j);
+        if (cp) issue_at(j, kc_src, kc_lds);
+        kc_src += dsrc;
+        kc_lds += C::SLOT_BYTES;
+        if (kc_lds == lds_wrap) kc_lds = lds_first;
         if (r < n_w)
             vphase(r, r >= n_um);
         else {
