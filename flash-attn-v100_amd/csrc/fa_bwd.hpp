@@ -83,6 +83,28 @@ __global__ __launch_bounds__(256) void delta_kernel(const BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// -x for eight 16-bit floats (the sign bits)
+__device__ FA_INLINE inline uint4 neg16x8(uint4 v) {
+    v.x ^= 0x80008000u;
+    v.y ^= 0x80008000u;
+    v.z ^= 0x80008000u;
+    v.w ^= 0x80008000u;
+    return v;
+}
+// delta of the 16 queries {8 g + 4 hi + e} of a 32-query sub-step in the
+// accumulator order of a lane (a key per lane), from the sub-step's LDS row
+__device__ FA_INLINE inline f32x16 delta16(const float* d, int hi) {
+    f32x16 r;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(d + 8 * g + 4 * hi);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[4 * g + e] = d4[e];
+    }
+    return r;
+}
+
+// ---------------------------------------------------------------------------
 template <typename T, int D>
 struct DkdvCfg {
     static constexpr bool F32 = Elem<T>::kF32;
@@ -125,6 +147,11 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
     constexpr bool BIAS = !std::is_void<TB>::value;
     using BT = typename std::conditional<BIAS, TB, T>::type;
     constexpr int BQ = C::BQ, RW = C::RW;
+    // 16-bit inputs without bias or dropout: the dP products start from delta
+    // and take -V, so they give delta - dP, and dS = P (dP - delta) costs one
+    // product a score; the products then sum -dS into dK (-scale at the end).
+    // (dkdv_pp_kernel does the same, bit for bit.)
+    constexpr bool DFOLD = !C::F32 && !BIAS && DROPOUT == 0;
     __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
 
     const int tid = threadIdx.x;
@@ -151,6 +178,10 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
             const bool ok = kj < p.Sk;
             kreg[i] = ok ? *reinterpret_cast<const uint4*>(krow + d0) : make_uint4(0u, 0u, 0u, 0u);
             vreg[i] = ok ? *reinterpret_cast<const uint4*>(vrow + d0) : make_uint4(0u, 0u, 0u, 0u);
+        }
+        if constexpr (DFOLD) {
+#pragma unroll
+            for (int i = 0; i < KR; ++i) vreg[i] = neg16x8(vreg[i]);
         }
     }
     // no wait here: the K / V loads stay in flight while the first tile copy
@@ -207,7 +238,10 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
         const T* Qs = (const T*)buf(s);
         const T* Ds = (const T*)(buf(s) + C::QALLOC);
         sc = f32x16{};
-        dpc = f32x16{};
+        if constexpr (DFOLD)
+            dpc = delta16((const float*)(buf(s) + 2 * C::QALLOC) + BQ + 32 * st, hi);
+        else
+            dpc = f32x16{};
         const T* qrow = Qs + (32 * st + l32) * RW;
         const T* drow = Ds + (32 * st + l32) * RW;
         if constexpr (C::F32) {
@@ -323,7 +357,10 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
                     pdv = keep ? pv : 0.f;
                 }
                 pd[r] = pdv;
-                ds[r] = DROPOUT ? pv * __builtin_fmaf(dpv, p.rp, -d4[e]) : pv * (dpv - d4[e]);
+                if constexpr (DFOLD)
+                    ds[r] = pv * dpv;  // -dS
+                else
+                    ds[r] = DROPOUT ? pv * __builtin_fmaf(dpv, p.rp, -d4[e]) : pv * (dpv - d4[e]);
             }
         }
         if (want_db) {
@@ -454,7 +491,7 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
     for (int pass = 0; pass < 2; ++pass) {
         sync_tiles();
         const f32x16* acc = pass == 0 ? dk : dv;
-        const float mul = pass == 0 ? p.scale : (DROPOUT ? p.rp : 1.f);
+        const float mul = pass == 0 ? (DFOLD ? -p.scale : p.scale) : (DROPOUT ? p.rp : 1.f);
 #pragma unroll
         for (int i = 0; i < DA / 32; ++i)
 #pragma unroll
@@ -573,6 +610,9 @@ __global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, cons
             kreg[i] = ok ? *reinterpret_cast<const uint4*>(krow + d0) : make_uint4(0u, 0u, 0u, 0u);
             vreg[i] = ok ? *reinterpret_cast<const uint4*>(vrow + d0) : make_uint4(0u, 0u, 0u, 0u);
         }
+        // -V: the dP products start from delta and give delta - dP (as dkdv_kernel)
+#pragma unroll
+        for (int i = 0; i < KR; ++i) vreg[i] = neg16x8(vreg[i]);
     }
     f32x16 dk[D / 32], dv[D / 32];
 #pragma unroll
@@ -730,7 +770,9 @@ __global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, cons
         const T* Da = (const T*)(slot(sa) + C::QALLOC) + 32 * sta * RW;
         const T* Qb = (const T*)slot(sb) + (32 * stb + l32) * RW + 8 * hi;
         const T* Db = (const T*)(slot(sb) + C::QALLOC) + (32 * stb + l32) * RW + 8 * hi;
+        const float* delb = (const float*)(slot(sb) + 2 * C::QALLOC) + BQ + 32 * stb;
         s16x8 x[NSTEP], y[NSTEP];
+        f32x16 dinit;  // delta of the sub-step's queries: the dP products start from it
         auto rd = [&](int t) FA_INLINE {
             if (t < NA) {
                 const int ks = t / (D / 32), i = t % (D / 32);
@@ -741,6 +783,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, cons
                 const int kk = t - NA;
                 x[t] = *reinterpret_cast<const s16x8*>(Qb + 16 * kk);
                 y[t] = *reinterpret_cast<const s16x8*>(Db + 16 * kk);
+                if (kk == 0) dinit = delta16(delb, hi);
             }
         };
         auto mm = [&](int t) FA_INLINE {
@@ -751,7 +794,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, cons
             } else {
                 const int kk = t - NA;
                 sc = Elem<T>::mfma(x[t], __builtin_bit_cast(s16x8, kreg[kk]), kk == 0 ? f32x16{} : sc);
-                dpc = Elem<T>::mfma(y[t], __builtin_bit_cast(s16x8, vreg[kk]), kk == 0 ? f32x16{} : dpc);
+                dpc = Elem<T>::mfma(y[t], __builtin_bit_cast(s16x8, vreg[kk]), kk == 0 ? dinit : dpc);
             }
         };
         constexpr int T0 = A ? 0 : NA, T1 = BB ? NSTEP : NA;
@@ -767,6 +810,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, cons
         auto rd_group = [&](int t) FA_INLINE {  // 4 transposing reads or 2 row reads
             if (t < NA)
                 __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            else if (t == NA)
+                __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);  // with the 4 delta reads
             else
                 __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         };
@@ -785,18 +830,16 @@ __global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, cons
     // that each produce P / dS make the register allocator spill)
     auto vphase = [&](int s, int st, int qs0, bool msk) FA_INLINE {
         const float* lse2 = (const float*)(slot(s) + 2 * C::QALLOC) + 32 * st;
-        const float* dels = lse2 + BQ;
         float pd[16], ds[16];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse2 + 8 * g + 4 * hi);
-            const f32x4 d4 = *reinterpret_cast<const f32x4*>(dels + 8 * g + 4 * hi);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int rr = 4 * g + e;
                 const float pv = fast_exp2(__builtin_fmaf(sc[rr], c, -l4[e]));
                 pd[rr] = pv;
-                ds[rr] = pv * (dpc[rr] - d4[e]);
+                ds[rr] = pv * dpc[rr];  // -dS (dpc = delta - dP)
             }
         }
         if (CAUSAL && msk) {
@@ -913,7 +956,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, cons
     for (int pass = 0; pass < 2; ++pass) {
         if (pass == 1) lds_barrier();  // this wave's dK rows are stored (its own region)
         const f32x16* acc = pass == 0 ? dk : dv;
-        const float mul = pass == 0 ? p.scale : 1.f;
+        const float mul = pass == 0 ? -p.scale : 1.f;  // the products summed -dS
 #pragma unroll
         for (int i = 0; i < D / 32; ++i)
 #pragma unroll
