@@ -1921,7 +1921,7 @@ __global__ __launch_bounds__(512, 1) void dq_pp_kernel(const BwdParams p) {
     constexpr int NA = (BN / 16) * (D / 32);  // dQ steps (one product each)
     constexpr int NB = 2 * QR;                // S/dP steps (an S and a dP product each)
     constexpr int NSTEP = NA + NB;
-    constexpr int MP = 2;
+    constexpr int MP = 3;
     s16x8 bs8[BN / 16];       // dS^T of the previous tile (B operands)
     f32x16 sc[2], dpc[2];     // S^T, dP^T of this tile, per 32-key block
     auto mphase = [&](int r, auto a_tag, auto b_tag) FA_INLINE {
