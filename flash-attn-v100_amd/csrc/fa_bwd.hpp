@@ -1924,6 +1924,18 @@ __global__ __launch_bounds__(512, 1) void dq_pp_kernel(const BwdParams p) {
     constexpr int MP = 3;
     s16x8 bs8[BN / 16];       // dS^T of the previous tile (B operands)
     f32x16 sc[2], dpc[2];     // S^T, dP^T of this tile, per 32-key block
+    // the first MP dQ steps' K^T operands of round r, read at the end of the
+    // previous V phase (tile r - 1 stays in its slot until round r + 2)
+    s16x8 xpre[MP];
+    auto prefetch = [&](int r) FA_INLINE {
+        const T* Ka = (const T*)slot(r + NSLOT - 1);
+#pragma unroll
+        for (int t = 0; t < MP; ++t) {
+            const int ks = t / (D / 32), i = t % (D / 32);
+            const T* kp = Ka + (16 * ks + trow) * KW + 32 * i + tcol;
+            xpre[t] = cat4(lds_read_tr16(kp), lds_read_tr16(kp + 8 * KW));
+        }
+    };
     auto mphase = [&](int r, auto a_tag, auto b_tag) FA_INLINE {
         constexpr bool A = decltype(a_tag)::value, BB = decltype(b_tag)::value;
         const T* Ka = (const T*)slot(r + NSLOT - 1);
@@ -1952,8 +1964,14 @@ __global__ __launch_bounds__(512, 1) void dq_pp_kernel(const BwdParams p) {
             }
         };
         constexpr int T0 = A ? 0 : NA, T1 = BB ? NSTEP : NA;
+        static_assert(MP <= NA, "prefetched steps are dQ steps");
 #pragma unroll
-        for (int t = T0; t < T0 + MP; ++t) rd(t);
+        for (int t = T0; t < T0 + MP; ++t) {
+            if (A)
+                x[t] = xpre[t];
+            else
+                rd(t);
+        }
 #pragma unroll
         for (int t = T0; t < T1; ++t) {
             if (t + MP < T1) rd(t + MP);
@@ -1970,8 +1988,10 @@ __global__ __launch_bounds__(512, 1) void dq_pp_kernel(const BwdParams p) {
             else
                 __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
         };
+        if (!A) {
 #pragma unroll
-        for (int t = T0; t < T0 + MP; ++t) rd_group(t);
+            for (int t = T0; t < T0 + MP; ++t) rd_group(t);
+        }
 #pragma unroll
         for (int t = T0; t < T1; ++t) {
             mf_group(t);
@@ -2061,6 +2081,7 @@ __global__ __launch_bounds__(512, 1) void dq_pp_kernel(const BwdParams p) {
 #pragma unroll
             for (int ks = 0; ks < BN / 16; ++ks) bs8[ks] = s16x8{};
         }
+        if (r + 1 <= n_tiles) prefetch(r + 1);
         if (!cp)
             wait_vmem();
         else if (n_copy == C::PER)
