@@ -1021,20 +1021,21 @@ struct Dkdv8Cfg {
     using KV = DmaTile<T, BK, D, KVW, NW>;
 };
 
+// (bid, nblocks: this workgroup among the dK/dV ones; smem: Dkdv8Cfg::SMEM_BYTES of LDS)
 template <typename T, int D, bool CAUSAL, typename TB>
-__global__ __launch_bounds__(512, 1) void dkdv8_kernel(const BwdParams p, const int n_ktiles) {
+__device__ FA_INLINE inline void dkdv8_body(const BwdParams& p, const int n_ktiles, const int bid, const int nblocks,
+                                           char* smem) {
     using C = Dkdv8Cfg<T, D>;
     static_assert(!Elem<T>::kF32, "16-bit inputs");
     constexpr bool BIAS = !std::is_void<TB>::value;
     using BT = typename std::conditional<BIAS, TB, T>::type;
     constexpr int BQ = C::BQ, RW = C::RW, KVW = C::KVW;
-    __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
     const int kb = w & 3;   // key block
     const int st = w >> 2;  // query sub-step of every tile
-    const int2 tord = tile_order<32>(n_ktiles);  // kt = 0 sees the most queries
+    const int2 tord = tile_order<32>(n_ktiles, bid, nblocks);  // kt = 0 sees the most queries
     const int bhk = tord.x;
     const int kt = tord.y;
     const int hk = bhk % p.Hkv, b = bhk / p.Hkv;
@@ -1328,6 +1329,13 @@ __global__ __launch_bounds__(512, 1) void dkdv8_kernel(const BwdParams p, const 
     }
 }
 
+template <typename T, int D, bool CAUSAL, typename TB>
+__global__ __launch_bounds__(512, 1) void dkdv8_kernel(const BwdParams p, const int n_ktiles) {
+    __shared__ __attribute__((aligned(16))) char smem[Dkdv8Cfg<T, D>::SMEM_BYTES];
+    dkdv8_body<T, D, CAUSAL, TB>(p, n_ktiles, (int)blockIdx.x, (int)gridDim.x, smem);
+}
+
+
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 struct DqCfg {
@@ -1355,22 +1363,22 @@ struct DqCfg {
 // KS: key split, as in fwd_kernel: KS groups of 4 waves on the same 128
 // queries, group sp walking key tiles sp, sp + KS, ... through its own LDS
 // buffers; their dQ partials are summed through LDS at the end (small grids).
+// (bid, nblocks: this workgroup among the dQ ones; smem: KS * DqCfg::SMEM_BYTES of LDS)
 template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB, int KS>
-__global__ __launch_bounds__(256 * KS, (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)) void dq_kernel(const BwdParams p,
-                                                                                           const int n_qtiles) {
+__device__ FA_INLINE inline void dq_body(const BwdParams& p, const int n_qtiles, const int bid, const int nblocks,
+                                        char* smem) {
     using C = DqCfg<T, D>;
     constexpr bool BIAS = !std::is_void<TB>::value;
     using BT = typename std::conditional<BIAS, TB, T>::type;
     using BT16 = typename std::conditional<C::F32, bf16, T>::type;  // the 16-bit input type
     constexpr int BN = C::BN, KW = C::KW;
-    __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES * KS];
 
     const int tid = threadIdx.x;
     // wave index as a scalar: loop bounds derived from it stay wave-uniform
     const int lane = tid & 63, wg = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
     // w: the wave's 32-query block, sp: its key split (compile-time 0 without one)
     const int w = KS == 1 ? wg : wg & 3, sp = KS == 1 ? 0 : wg >> 2;
-    const int2 tord = tile_order<32 * (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)>(n_qtiles);
+    const int2 tord = tile_order<32 * (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)>(n_qtiles, bid, nblocks);
     const int bh = tord.x;
     const int qt = n_qtiles - 1 - tord.y;  // longest causal rows first
     const int h = bh % p.H, b = bh / p.H;
@@ -1733,6 +1741,54 @@ __global__ __launch_bounds__(256 * KS, (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)) 
         }
     }
 }
+
+template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB, int KS>
+__global__ __launch_bounds__(256 * KS, (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)) void dq_kernel(const BwdParams p,
+                                                                                           const int n_qtiles) {
+    __shared__ __attribute__((aligned(16))) char smem[DqCfg<T, D>::SMEM_BYTES * KS];
+    dq_body<T, D, CAUSAL, DROPOUT, TB, KS>(p, n_qtiles, (int)blockIdx.x, (int)gridDim.x, smem);
+}
+
+// ---------------------------------------------------------------------------
+// A whole backward on a grid smaller than the CU count (16-bit inputs, D = 64
+// or 128, no bias or dropout), after the delta pre-pass: the dK/dV workgroups
+// (dkdv8_body) and the key-split dQ workgroups (dq_body, KS = 2) of the two
+// passes in one launch, interleaved longest first.  Each pass alone leaves CUs
+// idle and runs for the length of its longest workgroup's tile chain; together
+// they share the CUs and the two chains overlap.  Per element the arithmetic
+// is that of the two kernels (and of dq_kernel after the pre-pass), so the
+// outputs are bit-identical to running them one after the other.
+template <typename T, int D>
+struct BwdSmallCfg {
+    static constexpr int S1 = Dkdv8Cfg<T, D>::SMEM_BYTES, S2 = 2 * DqCfg<T, D>::SMEM_BYTES;
+    static constexpr int SMEM_BYTES = S1 > S2 ? S1 : S2;
+    static_assert(Dkdv8Cfg<T, D>::NT == 512 && 2 * DqCfg<T, D>::NT == 512, "one workgroup size");
+    static_assert(SMEM_BYTES <= 160 * 1024, "LDS of one CU");
+};
+
+template <typename T, int D, bool CAUSAL>
+__global__ __launch_bounds__(512, 1) void bwd_small_kernel(const BwdParams p, const int n_ktiles, const int n_kv,
+                                                          const int n_qtiles, const int n_q) {
+    __shared__ __attribute__((aligned(16))) char smem[BwdSmallCfg<T, D>::SMEM_BYTES];
+    // workgroups 2 i and 2 i + 1 take the i-th dK/dV and dQ ones while both
+    // kinds last, then the rest of the larger kind
+    const int b = (int)blockIdx.x;
+    const int m = min(n_kv, n_q);
+    bool kv;
+    int idx;
+    if (b < 2 * m) {
+        kv = (b & 1) == 0;
+        idx = b >> 1;
+    } else {
+        kv = n_kv > n_q;
+        idx = m + (b - 2 * m);
+    }
+    if (kv)
+        dkdv8_body<T, D, CAUSAL, void>(p, n_ktiles, idx, n_kv, smem);
+    else
+        dq_body<T, D, CAUSAL, 0, void, 2>(p, n_qtiles, idx, n_q, smem);
+}
+
 
 // ---------------------------------------------------------------------------
 // Ping-pong dQ for 16-bit inputs without bias or dropout, D = 128, on grids
@@ -2373,8 +2429,39 @@ inline bool dq_pp_runs(const BwdParams& p) {
     return nb >= 256;
 }
 
+// Whether the whole backward runs as the delta pre-pass plus bwd_small_kernel
+// (16-bit inputs, D = 64 or 128, no bias or dropout): where dK/dV would run
+// dkdv8_kernel on fewer workgroups than CUs and dQ the key-split dq_kernel,
+// and either both kinds of workgroups fit the CUs at once or the mask makes
+// their tile chains uneven (non-causal chains of one length on more workgroups
+// than CUs gain nothing from sharing them and would pay the pre-pass).
+template <typename T, int D, bool CAUSAL>
+inline bool bwd_small_runs(const BwdParams& p) {
+    if constexpr (!Elem<T>::kF32 && (D == 64 || D == 128) && 2 * DqCfg<T, D>::SMEM_BYTES <= 160 * 1024) {
+        const int64_t nq = (int64_t)((p.Sq + DqCfg<T, D>::BM - 1) / DqCfg<T, D>::BM) * p.H * p.B;
+        const int64_t nkv = (int64_t)((p.Sk + Dkdv8Cfg<T, D>::BK - 1) / Dkdv8Cfg<T, D>::BK) * p.Hkv * p.B;
+        return dkdv8_runs<T, D, CAUSAL, 0, void>(p) && nq > 0 && nq < 256 && p.Sk > DqCfg<T, D>::BN &&
+               (CAUSAL || nq + nkv <= 256);
+    }
+    return false;
+}
+
 template <typename T, int D, bool CAUSAL, int DROPOUT, typename TB>
 hipError_t launch_bwd_t(const BwdParams& p0, int stage, hipStream_t s) {
+    if constexpr (!Elem<T>::kF32 && DROPOUT == 0 && std::is_void<TB>::value && (D == 64 || D == 128)) {
+        if (stage < 0 && bwd_small_runs<T, D, CAUSAL>(p0)) {
+            hipError_t e = launch_bwd_t<T, D, CAUSAL, DROPOUT, TB>(p0, 0, s);  // delta rows
+            if (e != hipSuccess) return e;
+            BwdParams pr = p0;
+            pr.dq_delta = 0;  // dQ reads the delta rows
+            const int nk = (p0.Sk + Dkdv8Cfg<T, D>::BK - 1) / Dkdv8Cfg<T, D>::BK;
+            const int nq = (p0.Sq + DqCfg<T, D>::BM - 1) / DqCfg<T, D>::BM;
+            const int n_kv = nk * p0.Hkv * p0.B, n_q = nq * p0.H * p0.B;
+            hipLaunchKernelGGL((bwd_small_kernel<T, D, CAUSAL>), dim3((unsigned)(n_kv + n_q)), dim3(512), 0, s, pr, nk,
+                               n_kv, nq, n_q);
+            return hipGetLastError();
+        }
+    }
     // stage 3: the workspace rows and dQ, for a dQ pass that recomputes dS.
     // 16-bit inputs do both in the dQ kernel (no delta pre-pass); fp32 runs
     // the pre-pass, then the dQ pass.  The whole backward without a dS pass

@@ -333,12 +333,14 @@ __device__ FA_INLINE inline int xcd_remap(int L, int N) {
 // x resident workgroups per CU; measured against once and 4 times), so the
 // resident workgroups span few slices (K / V / Q tiles shared through the
 // XCD's L2), and a group never spans two XCDs.
+// (bid, nblocks: the workgroup's index among the nblocks of its kind, for a
+// launch that runs two kinds of workgroups)
 template <int SLOTS>
-__device__ FA_INLINE inline int2 tile_order(int n_tiles) {
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
-    const int n_slices = gridDim.x / n_tiles;
+__device__ FA_INLINE inline int2 tile_order(int n_tiles, int bid, int nblocks) {
+    const int L = xcd_remap(bid, nblocks);
+    const int n_slices = nblocks / n_tiles;
     // groups stay inside one XCD's share of the slices
-    const int xcd_slices = max(1, (int)(gridDim.x >> 3) / n_tiles);
+    const int xcd_slices = max(1, (nblocks >> 3) / n_tiles);
     const int G = max(1, min(xcd_slices, (2 * SLOTS + n_tiles - 1) / n_tiles));
     const int per_group = G * n_tiles;
     const int g = L / per_group;
@@ -346,6 +348,10 @@ __device__ FA_INLINE inline int2 tile_order(int n_tiles) {
     const int gg = min(G, n_slices - g * G);  // the last group may be smaller
     const int rank = r / gg;
     return make_int2(g * G + (r - rank * gg), rank);
+}
+template <int SLOTS>
+__device__ FA_INLINE inline int2 tile_order(int n_tiles) {
+    return tile_order<SLOTS>(n_tiles, (int)blockIdx.x, (int)gridDim.x);
 }
 
 // ---------------------------------------------------------------------------

@@ -255,6 +255,38 @@ def test_bwd_stage3_equals_prepass_then_dq(dt, D):
     assert torch.equal(outs[0][1], outs[1][1])
 
 
+@pytest.mark.parametrize("case", [
+    # dtype, B, S, H, Hkv, D, causal: small grids (fewer dK/dV and dQ workgroups
+    # than CUs each); the first three run as the delta pre-pass plus one launch
+    # of both kinds of workgroups (causal, or both kinds fit the CUs at once)
+    (torch.float16, 2, 1024, 12, 12, 64, True),    # C2
+    (torch.bfloat16, 2, 777, 8, 8, 128, False),    # 112 + 112 workgroups
+    (torch.bfloat16, 1, 1000, 8, 2, 64, True),     # GQA 4:1, ragged tiles
+    (torch.float16, 2, 1024, 12, 12, 64, False),   # 384 workgroups, non-causal: two passes
+])
+def test_small_grid_bwd_equals_the_two_passes(case):
+    # fa_bwd on a small grid equals stage 3 (dQ with the delta rows) followed by
+    # stage 1 (dK/dV) bit for bit, whichever way it schedules the two passes
+    import ctypes
+    dt, B, S, H, Hkv, D, causal = case
+    say(f"case: small-grid fa_bwd vs stages 3 + 1, {case}")
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, S, H, D, dt, Hkv=Hkv, seed=41))
+    scale = D ** -0.5
+    o, lse, _ = _lib.fwd(q, k, v, causal, scale)
+    ref = _lib.bwd(q, k, v, o, do, lse, causal, scale)
+    lib = _lib.load()
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    a = _lib.bwd_args(q, k, v, o, do, lse, dq, dk, dv, causal, scale, 0.0, 0, 0)
+    ws = torch.empty(lib.fa_bwd_workspace_size(ctypes.byref(a)), device=DEV, dtype=torch.uint8)
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for st in (3, 1):
+        assert lib.fa_bwd_stage(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), st, sp) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(dq, ref[0]) and torch.equal(dk, ref[1]) and torch.equal(dv, ref[2])
+    res = compare(q, k, v, do, causal, scale, (o, lse) + tuple(ref), hpc=8)
+    assert_parity(res, dt, str(case))
+
+
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_bwd_stages_on_two_streams(with_bias):
     # include/fa_abi.h: after stage 0, stages 1 (dK/dV) and 2 (dQ) are
