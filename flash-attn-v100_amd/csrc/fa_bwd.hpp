@@ -17,6 +17,11 @@
 //      delta held per lane; 64-key K/V tiles are copied global -> LDS
 //      (double-buffered) and consumed as two 32-key sub-steps, K^T read from
 //      the K tile with transposing reads.
+// Variants of the same arithmetic: dkdv8_kernel (K and V in LDS, 8 waves: small
+// grids and a bias), dkdv_pp_kernel / dq_pp_kernel (8-wave ping-pong workgroups
+// of 256 keys / queries: 16-bit D = 128 grids that fill the chip),
+// bwd_small_kernel (the dK/dV and dQ workgroups of a small grid in one launch),
+// dq_ds_kernel (dQ from the dS a bias-gradient pass stored).
 // Diagonal (causal) tiles run a separate masking variant of each tile step.
 // With an additive bias (BIAS) both kernels add bias * log2 e to the scores
 // before the exponent; dkdv_kernel, the one kernel that visits every
