@@ -1561,6 +1561,9 @@ __device__ FA_INLINE inline void dq_body(const BwdParams& p, const int n_qtiles,
             }
             // ---- dS^T = P^T (dP^T - delta); scale applied at the end ----
             const bool need_mask = MASK && ((k0 + BN > p.Sk) || (CAUSAL && k0 + BN - 1 > qw0));
+            // key k0 + 4 hi + o (o = 8 (r / 4) + r % 4) is masked when it is >= Sk
+            // or (causal) > qi: one per-lane bound against constants
+            const int lim = (CAUSAL ? min(p.Sk, qi + 1) : p.Sk) - k0 - 4 * hi;
             // stored keep bits: key k0 + 8 g + 4 hi + e at bit 8 g + e after the shift
             const uint32_t km = DROPOUT == 2 ? kword >> (4 * hi) : 0u;
 #pragma unroll
@@ -1571,7 +1574,7 @@ __device__ FA_INLINE inline void dq_body(const BwdParams& p, const int n_qtiles,
                     pv = fast_exp2(__builtin_fmaf(s[r], c, __builtin_fmaf(bias_f32<BT>(bv[r >> 2][r & 3]), kLog2e, -lse2)));
                 else
                     pv = fast_exp2(__builtin_fmaf(s[r], c, -lse2));
-                if (need_mask && (key >= p.Sk || (CAUSAL && key > qi))) pv = 0.f;
+                if (need_mask && 8 * (r >> 2) + (r & 3) >= lim) pv = 0.f;
                 if (DROPOUT) {
                     const uint32_t m = DROPOUT == 2 ? bit_mask(km, 8 * (r >> 2) + (r & 3))
                                        : (philox_keep(p.seed, row_ctr + (uint64_t)key, p.keep_thresh) ? ~0u : 0u);
@@ -1632,11 +1635,11 @@ __device__ FA_INLINE inline void dq_body(const BwdParams& p, const int n_qtiles,
     auto fin16 = [&](int k0, const T* Ks, f32x16& s, const f32x16& dp, auto mask_tag) FA_INLINE {
         constexpr bool MASK = decltype(mask_tag)::value;
         const bool need_mask = MASK && ((k0 + 32 > p.Sk) || (CAUSAL && k0 + 31 > qw0));
+        const int lim = (CAUSAL ? min(p.Sk, qi + 1) : p.Sk) - k0 - 4 * hi;  // as in `sub`
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int key = k0 + 8 * (r >> 2) + 4 * hi + (r & 3);
             float pv = fast_exp2(__builtin_fmaf(s[r], c, -lse2));
-            if (need_mask && (key >= p.Sk || (CAUSAL && key > qi))) pv = 0.f;
+            if (need_mask && 8 * (r >> 2) + (r & 3) >= lim) pv = 0.f;
             s[r] = pv * (dp[r] - del);
         }
         const int trow = 4 * hi + ((lane & 15) >> 2);

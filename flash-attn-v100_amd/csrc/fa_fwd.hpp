@@ -263,13 +263,14 @@ __global__ __launch_bounds__(256 * KS * QG, KS == 1 && QG == 1 && D <= 128 ? 2 :
     auto mask = [&](f32x16 (&s)[NB], int k0) {
         const bool need = (k0 + BN > p.Sk) || (CAUSAL && k0 + BN - 1 > qw0);
         if (need) {
+            // key k0 + 4 hi + o (o = 32 blk + 8 (r / 4) + r % 4) is masked when it is
+            // >= Sk or (causal) > qi: one per-lane bound against constants
+            const int lim = (CAUSAL ? min(p.Sk, qi + 1) : p.Sk) - k0 - 4 * hi;
 #pragma unroll
             for (int blk = 0; blk < NB; ++blk)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = k0 + 32 * blk + 8 * (r >> 2) + 4 * hi + (r & 3);
-                    if (key >= p.Sk || (CAUSAL && key > qi)) s[blk][r] = -INFINITY;
-                }
+                for (int r = 0; r < 16; ++r)
+                    if (32 * blk + 8 * (r >> 2) + (r & 3) >= lim) s[blk][r] = -INFINITY;
         }
     };
     // running max; O and l are rescaled (lazily: only when the max grows by
@@ -749,16 +750,17 @@ __global__ __launch_bounds__(576, 1) void fwd_pp_kernel(const FwdParams p) {
     };
 
     // ---- V phase of tile r: mask, running max (lazy rescale), P(r) ----
+    const int lim0 = (CAUSAL ? min(p.Sk, qi + 1) : p.Sk) - 4 * hi;
     auto vphase = [&](int r) FA_INLINE {
         if (r >= n_um) {
-            const int k0 = r * BN;
+            // key r BN + 4 hi + o (o = 32 bk + 8 (e / 4) + e % 4) is masked when it
+            // is >= Sk or (causal) > qi: one per-lane bound against constants
+            const int lim = lim0 - r * BN;
 #pragma unroll
             for (int bk = 0; bk < NB; ++bk)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int key = k0 + 32 * bk + 8 * (e >> 2) + 4 * hi + (e & 3);
-                    if (key >= p.Sk || (CAUSAL && key > qi)) s[bk][e] = -INFINITY;
-                }
+                for (int e = 0; e < 16; ++e)
+                    if (32 * bk + 8 * (e >> 2) + (e & 3) >= lim) s[bk][e] = -INFINITY;
         }
         float mx = -INFINITY;
 #pragma unroll
