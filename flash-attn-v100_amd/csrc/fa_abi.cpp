@@ -256,8 +256,17 @@ int32_t check_bias(const void* bias, const int64_t st[4], int32_t bias_dtype, in
 bool dbias_reduced(const fa_bwd_args* a) {
     return a->dbias && ((a->dbias_stride[0] == 0 && a->batch > 1) || (a->dbias_stride[1] == 0 && a->num_heads > 1));
 }
-// key row length of the parts: Sk rounded up to 4 (16-byte rows)
-int32_t dbias_part_row(int32_t Sk) { return (Sk + 3) / 4 * 4; }
+// Element type of the parts: the gradient's own dtype when it is the 16-bit
+// input dtype (each part rounded once to it, as the unsummed gradient is; the
+// dQ pass then reads its dS at half the bytes), float32 otherwise.
+int32_t dbias_part_dtype(const fa_bwd_args* a) {
+    return a->dtype != FA_DTYPE_F32 && a->dbias_dtype == a->dtype ? a->dtype : FA_DTYPE_F32;
+}
+// key row length of the parts: Sk rounded up to whole 16-byte rows
+int32_t dbias_part_row(const fa_bwd_args* a) {
+    const int32_t per16 = 16 / elem_size(dbias_part_dtype(a));
+    return (a->seqlen_k + per16 - 1) / per16 * per16;
+}
 
 // Optional bias gradient: dtype fp16, bf16 or fp32; j stride 1, i stride >= Sk
 // (rows do not overlap: stores past the last row must leave the slice),
@@ -279,12 +288,13 @@ int32_t check_dbias(const fa_bwd_args* a) {
         if (!aligned16(dbias)) return FA_ERR_BIAS;
         for (int i = 0; i < 3; ++i)
             if (st[i] % 4 != 0) return FA_ERR_BIAS;
-        const int64_t part_st[4] = {0, 0, dbias_part_row(a->seqlen_k), 1};
-        if (check_slice_offsets(part_st, a->seqlen_q, a->seqlen_k, 4)) return FA_ERR_TOO_LARGE;
-        // the float32 parts of every (batch, head) must be addressable (and their
+        const int pes = elem_size(dbias_part_dtype(a));
+        const int64_t part_st[4] = {0, 0, dbias_part_row(a), 1};
+        if (check_slice_offsets(part_st, a->seqlen_q, a->seqlen_k, pes)) return FA_ERR_TOO_LARGE;
+        // the parts of every (batch, head) must be addressable (and their
         // workspace size representable)
         const int64_t parts = mul_capped(mul_capped((int64_t)a->batch * a->num_heads, a->seqlen_q),
-                                         (int64_t)dbias_part_row(a->seqlen_k) * 4);
+                                         (int64_t)dbias_part_row(a) * pes);
         if (parts < 0) return FA_ERR_TOO_LARGE;
     }
     return check_slice_offsets(st, a->seqlen_q, a->seqlen_k, es);
@@ -292,8 +302,8 @@ int32_t check_dbias(const fa_bwd_args* a) {
 
 // Backward workspace: B * H rows of 2 * sq_pad float32 (LSE * log2 e, then
 // delta), sq_pad = Sq rounded up to kSqPad, rounded up to 256 bytes; then,
-// for a summed bias gradient, the (B, H, Sq, Sk rounded up to 4) float32
-// parts, rounded up to 256 bytes.
+// for a summed bias gradient, the (B, H, Sq, Sk rounded up to 16 bytes)
+// parts (dbias_part_dtype), rounded up to 256 bytes.
 size_t ws_rows_bytes(const fa_bwd_args* a) {
     const size_t sq_pad = ((size_t)a->seqlen_q + fa::kSqPad - 1) / fa::kSqPad * fa::kSqPad;
     const size_t n = (size_t)a->batch * (size_t)a->num_heads * 2 * sq_pad * sizeof(float);
@@ -302,7 +312,8 @@ size_t ws_rows_bytes(const fa_bwd_args* a) {
 size_t ws_bytes_for(const fa_bwd_args* a) {
     size_t n = ws_rows_bytes(a);
     if (dbias_reduced(a)) {
-        const size_t parts = (size_t)a->batch * a->num_heads * a->seqlen_q * dbias_part_row(a->seqlen_k) * 4;
+        const size_t parts = (size_t)a->batch * a->num_heads * a->seqlen_q * dbias_part_row(a) *
+                             elem_size(dbias_part_dtype(a));
         n += (parts + 255) & ~(size_t)255;
     }
     return n;
@@ -534,17 +545,19 @@ int32_t bwd_run(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int32_t 
     const bool reduce_db = dbias_reduced(a);
     fa::DbiasReduceParams rp{};
     if (reduce_db) {  // parts in the workspace, summed into dbias after dK/dV
-        const int SkP = dbias_part_row(a->seqlen_k);
+        const int SkP = dbias_part_row(a);
+        const int32_t pdt = dbias_part_dtype(a);
         const int64_t part_st[4] = {(int64_t)a->num_heads * a->seqlen_q * SkP, (int64_t)a->seqlen_q * SkP, SkP, 1};
         p.dbias = (char*)workspace + ws_rows_bytes(a);
         p.dbias_sb = part_st[0];
         p.dbias_sh = part_st[1];
         p.dbias_ss = part_st[2];
-        p.dbias_span = slice_span(part_st, a->seqlen_q, a->seqlen_k, 4);
-        p.dbias_dtype = FA_DTYPE_F32;
-        p.dbias_es = 4;
+        p.dbias_dtype = pdt;
+        p.dbias_es = elem_size(pdt);
+        p.dbias_span = slice_span(part_st, a->seqlen_q, a->seqlen_k, p.dbias_es);
         p.dbias_zero_fill = 0;
-        rp.part = (const float*)p.dbias;
+        rp.part = p.dbias;
+        rp.part_dtype = pdt;
         rp.out = a->dbias;
         rp.out_dtype = a->dbias_dtype;
         rp.out_sb = a->dbias_stride[0];
@@ -569,14 +582,15 @@ int32_t bwd_run(const fa_bwd_args* a, void* workspace, size_t ws_bytes, int32_t 
         p.dbias_zero_fill = 1;
     }
     // dQ from the stored dS: 16-bit inputs, dS in their dtype or float32, whole
-    // 16-byte chunks (the summed form's float32 parts always qualify: their rows
-    // are Sk rounded up to 4 floats, and the readable span covers whole rows)
+    // 16-byte chunks (the summed form's parts always qualify: they are in the
+    // input dtype or float32, their rows are whole 16-byte chunks, and the
+    // readable span covers whole rows)
     p.dq_from_ds = 0;
     p.ds_span = 0;
     if (a->dbias && a->dtype != FA_DTYPE_F32) {
         if (reduce_db) {
             p.dq_from_ds = 1;
-            p.ds_span = (int)std::min<int64_t>((int64_t)a->seqlen_q * dbias_part_row(a->seqlen_k) * 4, 0x7fffffff);
+            p.ds_span = (int)std::min<int64_t>((int64_t)a->seqlen_q * dbias_part_row(a) * p.dbias_es, 0x7fffffff);
         } else {
             const int64_t es = p.dbias_es;
             const bool chunks = aligned16(a->dbias) && (p.dbias_sb * es) % 16 == 0 && (p.dbias_sh * es) % 16 == 0 &&

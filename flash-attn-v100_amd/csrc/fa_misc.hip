@@ -3,6 +3,7 @@
 // gradient and the zero tails of a causal bias gradient.
 #include <algorithm>
 
+#include "fa_abi.h"
 #include "fa_common.hpp"
 #include "fa_params.hpp"
 
@@ -93,66 +94,79 @@ hipError_t launch_keep_bits(const FwdParams& p, bool causal, hipStream_t s) {
     return hipGetLastError();
 }
 
-// One thread per 4 consecutive keys of one output row: 16-byte loads of
-// every part slice that sums into it (HBM-bound streaming, no atomics).
+// One thread per 16 bytes of part keys of one output row (KPT = 4 float32
+// or 8 16-bit keys): one 16-byte load of every part slice that sums into it,
+// summed in float32 in slice order (HBM-bound streaming, no atomics).  Part
+// rows are whole 16-byte chunks (Sk rounded up); 16-bit parts have the output's
+// dtype.
+template <int KPT>
 __global__ __launch_bounds__(256) void dbias_reduce_kernel(const DbiasReduceParams r) {
-    const int nj4 = (r.Sk + 3) >> 2;
+    const int njg = (r.Sk + KPT - 1) / KPT;
     const int Bo = r.sum_b ? 1 : r.B, Ho = r.sum_h ? 1 : r.H;
-    const int64_t n = (int64_t)Bo * Ho * r.Sq * nj4;
+    const int64_t n = (int64_t)Bo * Ho * r.Sq * njg;
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (t >= n) return;
-    const int j = (int)(t % nj4) * 4;
-    int64_t rest = t / nj4;
+    const int j = (int)(t % njg) * KPT;
+    int64_t rest = t / njg;
     const int i = (int)(rest % r.Sq);
     rest /= r.Sq;
     const int ho = (int)(rest % Ho), bo = (int)(rest / Ho);
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float acc[KPT];
+    for (int e = 0; e < KPT; ++e) acc[e] = 0.f;
     if (!r.causal || j <= i) {
         const int b0 = r.sum_b ? 0 : bo, b1 = r.sum_b ? r.B : bo + 1;
         const int h0 = r.sum_h ? 0 : ho, h1 = r.sum_h ? r.H : ho + 1;
         for (int b = b0; b < b1; ++b)
             for (int h = h0; h < h1; ++h) {
-                const float4 v = *reinterpret_cast<const float4*>(
-                    r.part + (((int64_t)b * r.H + h) * r.Sq + i) * r.SkP + j);
-                acc.x += v.x;
-                acc.y += v.y;
-                acc.z += v.z;
-                acc.w += v.w;
+                const int64_t pe = (((int64_t)b * r.H + h) * r.Sq + i) * r.SkP + j;  // element index
+                const uint4 u = *reinterpret_cast<const uint4*>((const char*)r.part + pe * (16 / KPT));
+                if constexpr (KPT == 4) {
+                    const f32x4 v = __builtin_bit_cast(f32x4, u);
+                    for (int e = 0; e < 4; ++e) acc[e] += v[e];
+                } else {
+                    const s16x8 v = __builtin_bit_cast(s16x8, u);
+                    for (int e = 0; e < 8; ++e)
+                        acc[e] += r.part_dtype == FA_DTYPE_BF16 ? Elem<bf16>::unpack1(v[e]) : Elem<f16>::unpack1(v[e]);
+                }
             }
-        if (r.causal) {  // the part entries past the diagonal were never written
-            if (j + 1 > i) acc.y = 0.f;
-            if (j + 2 > i) acc.z = 0.f;
-            if (j + 3 > i) acc.w = 0.f;
-        }
+        if (r.causal)  // the part entries past the diagonal were never written
+            for (int e = 1; e < KPT; ++e)
+                if (j + e > i) acc[e] = 0.f;
     }
     const int64_t oe = bo * r.out_sb + ho * r.out_sh + (int64_t)i * r.out_ss + j;  // element index
-    const float a[4] = {acc.x, acc.y, acc.z, acc.w};
-    const int n_out = min(4, r.Sk - j);
-    if (r.out_dtype == 2) {
+    const int n_out = min(KPT, r.Sk - j);
+    if (r.out_dtype == FA_DTYPE_F32) {
         float* o = (float*)r.out + oe;
-        if (n_out == 4)
-            *reinterpret_cast<float4*>(o) = acc;
+        if (n_out == KPT)
+            for (int e = 0; e < KPT; e += 4)
+                *reinterpret_cast<float4*>(o + e) = make_float4(acc[e], acc[e + 1], acc[e + 2], acc[e + 3]);
         else
-            for (int e = 0; e < n_out; ++e) o[e] = a[e];
+            for (int e = 0; e < n_out; ++e) o[e] = acc[e];
     } else {
-        unsigned short h[4];
-        for (int e = 0; e < 4; ++e)
-            h[e] = r.out_dtype == 1 ? __builtin_bit_cast(unsigned short, (bf16)a[e])
-                                    : __builtin_bit_cast(unsigned short, (f16)a[e]);
+        unsigned short h[KPT];
+        for (int e = 0; e < KPT; ++e)
+            h[e] = r.out_dtype == FA_DTYPE_BF16 ? __builtin_bit_cast(unsigned short, (bf16)acc[e])
+                                                : __builtin_bit_cast(unsigned short, (f16)acc[e]);
         unsigned short* o = (unsigned short*)r.out + oe;
-        if (n_out == 4)
-            *reinterpret_cast<uint2*>(o) = make_uint2(h[0] | (unsigned)h[1] << 16, h[2] | (unsigned)h[3] << 16);
+        if (n_out == KPT)  // 8-byte stores: the output's base and strides are multiples of 4 elements
+            for (int e = 0; e < KPT; e += 4)
+                *reinterpret_cast<uint2*>(o + e) =
+                    make_uint2(h[e] | (unsigned)h[e + 1] << 16, h[e + 2] | (unsigned)h[e + 3] << 16);
         else
             for (int e = 0; e < n_out; ++e) o[e] = h[e];
     }
 }
 
 hipError_t launch_dbias_reduce(const DbiasReduceParams& r, hipStream_t s) {
-    const int64_t n = (int64_t)(r.sum_b ? 1 : r.B) * (r.sum_h ? 1 : r.H) * r.Sq * ((r.Sk + 3) / 4);
+    const int kpt = r.part_dtype == FA_DTYPE_F32 ? 4 : 8;
+    const int64_t n = (int64_t)(r.sum_b ? 1 : r.B) * (r.sum_h ? 1 : r.H) * r.Sq * ((r.Sk + kpt - 1) / kpt);
     if (n <= 0) return hipSuccess;
     const int64_t nb = (n + 255) / 256;
     if (nb > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(dbias_reduce_kernel, dim3((unsigned)nb), dim3(256), 0, s, r);
+    if (kpt == 4)
+        hipLaunchKernelGGL(dbias_reduce_kernel<4>, dim3((unsigned)nb), dim3(256), 0, s, r);
+    else
+        hipLaunchKernelGGL(dbias_reduce_kernel<8>, dim3((unsigned)nb), dim3(256), 0, s, r);
     return hipGetLastError();
 }
 

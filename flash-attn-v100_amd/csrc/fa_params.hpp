@@ -101,7 +101,8 @@ struct BwdParams {
 // entries (j > i) are written as 0 without being read (the dK/dV kernel
 // leaves the parts of skipped query tiles unwritten).
 struct DbiasReduceParams {
-    const float* part;
+    const void* part;
+    int part_dtype;  // 0 fp16, 1 bf16, 2 fp32
     void* out;
     int out_dtype;  // 0 fp16, 1 bf16, 2 fp32
     int64_t out_sb, out_sh, out_ss;

@@ -131,8 +131,10 @@ typedef struct fa_fwd_args {
  * dbias_dtype (computed in float32, rounded once) (the reference returned
  * zeros, ops/attention.py:297-301).  A zero b or h stride of dbias sums the
  * gradient over that dimension (the gradient of a bias broadcast over it):
- * the workspace then also holds the float32 per-(b, h) parts, and dbias needs
- * a 16-byte aligned base and strides that are multiples of 4. */
+ * the workspace then also holds the per-(b, h) parts (in dbias_dtype when it
+ * is the 16-bit input dtype, each part rounded once and the parts summed in
+ * float32; float32 parts otherwise), and dbias needs a 16-byte aligned base
+ * and strides that are multiples of 4. */
 typedef struct fa_bwd_args {
     const void* q;
     const void* k;
@@ -190,8 +192,9 @@ int32_t fa_fwd(const fa_fwd_args* args, void* hip_stream);
 /* Bytes of device workspace fa_bwd needs: B * H rows of 2 * sq_pad float32
  * (sq_pad = Sq rounded up to 128; LSE * log2 e then delta = rowsum(dO * O),
  * written by the pre-pass), rounded up to 256 bytes; plus, for a summed
- * dbias, B * H * Sq * (Sk rounded up to 4) float32 parts, rounded up to 256
- * bytes; 0 on invalid arguments.
+ * dbias, B * H * Sq * Skp parts (dbias_dtype when it is the 16-bit input
+ * dtype, Skp = Sk rounded up to 8; float32 otherwise, Skp = Sk rounded up to
+ * 4), rounded up to 256 bytes; 0 on invalid arguments.
  * The reference had no workspace (it recomputed delta per tile pair,
  * backward_kernel.py:119-121). */
 size_t fa_bwd_workspace_size(const fa_bwd_args* args);

@@ -247,13 +247,16 @@ static void bwd_paths() {
     b.dbias_stride[2] = 72;
     const size_t wsb = fa_bwd_workspace_size(&b);
     const size_t rows = (size_t)(3 * 4 * 2 * 128 * 4 + 255) / 256 * 256;
-    CHECK(wsb == rows + (size_t)(3 * 4 * 70 * 72 * 4 + 255) / 256 * 256);
+    // the parts are in the gradient's dtype (fp16, the input dtype): rows of Sk
+    // rounded up to 8 elements
+    CHECK(wsb == rows + (size_t)(3 * 4 * 70 * 72 * 2 + 255) / 256 * 256);
     const int r0 = g_stub.reduce_calls;
     // dQ reads the stored dS here: it cannot run as the first pass (stage 3)
     CHECK(fa_bwd_stage(&b, alloc(wsb), wsb, 3, nullptr) == FA_ERR_SHAPE);
     CHECK(fa_bwd(&b, alloc(wsb), wsb, nullptr) == FA_OK);
     CHECK(g_stub.reduce_calls == r0 + 1 && g_stub.reduce.sum_b == 1 && g_stub.reduce.sum_h == 0);
-    CHECK(g_stub.reduce.SkP == 72 && g_stub.bwd.dbias_dtype == FA_DTYPE_F32 && g_stub.bwd.dbias_zero_fill == 0);
+    CHECK(g_stub.reduce.SkP == 72 && g_stub.reduce.part_dtype == FA_DTYPE_F16 && g_stub.bwd.dbias_dtype == FA_DTYPE_F16 &&
+          g_stub.bwd.dbias_es == 2 && g_stub.bwd.dbias_zero_fill == 0);
     CHECK(std::strcmp(g_stub.last, "launch_bwd_bias_f16") == 0);
     // a causal gradient written in place (dS read back by the dQ pass): the whole
     // backward writes the zero tails on the library's side stream when it can

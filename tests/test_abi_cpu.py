@@ -442,7 +442,8 @@ def test_reduce_dbias_sums_broadcast_dims():
 
 def test_summed_dbias_workspace_and_rules():
     # a zero batch/head stride of dbias sums the gradient; the workspace then
-    # also holds the (B, H, Sq, Sk rounded up to 4) float32 parts
+    # also holds the (B, H, Sq, Sk rounded up to 4) float32 parts of a float32
+    # gradient (a gradient in the 16-bit input dtype: below)
     lib = _lib.load()
     B, S, H, D, Sk = 2, 100, 3, 64, 98
     q = torch.zeros(B, S, H, D, dtype=torch.bfloat16)
@@ -461,3 +462,10 @@ def test_summed_dbias_workspace_and_rules():
     assert lib.fa_bwd_check(ctypes.byref(a), base) == CODES["FA_ERR_WORKSPACE"]
     a.dbias_stride[2] = 99  # summed rows must hold 16-byte groups of keys
     assert lib.fa_bwd_check(ctypes.byref(a), ws) == CODES["FA_ERR_BIAS"]
+    # a bf16 gradient (the input dtype): bf16 parts, rows of Sk rounded up to 8
+    summed16 = torch.zeros(1, H, S, 104, dtype=torch.bfloat16)[..., :Sk]
+    a = _lib.bwd_args(q, k, k, q, q, lse, q, k, k, True, 0.125, 0.0, 0, 0, pb, summed16)
+    ws16 = lib.fa_bwd_workspace_size(ctypes.byref(a))
+    assert ws16 == base + ((B * H * S * 104 * 2 + 255) // 256) * 256
+    assert lib.fa_bwd_check(ctypes.byref(a), ws16) == CODES["FA_OK"]
+    assert lib.fa_bwd_check(ctypes.byref(a), ws16 - 256) == CODES["FA_ERR_WORKSPACE"]
