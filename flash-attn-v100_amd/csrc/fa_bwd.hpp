@@ -1098,7 +1098,11 @@ __device__ FA_INLINE inline void dkdv8_body(const BwdParams& p, const int n_ktil
     };
     // the loop's barrier: the copies of the tile are done once at most the
     // NBL bias loads issued after them are in flight (vector loads complete in
-    // order; the dBias stores issued between them only add to the count)
+    // order; the dBias stores, issued before the copies, only add to the
+    // count).  A partial wait may count only loads issued after the ones it
+    // guards: stores complete out of order with respect to loads (issued
+    // after the copies and counted in the wait, the dS stores let the barrier
+    // pass with copies in flight: NaN in dK and dBias at B=4, S=4096)
     constexpr int NBL = BIAS ? 16 : 0;
     auto sync_copies = [&]() {
         wait_vmem_below<NBL>();
