@@ -1100,9 +1100,9 @@ __device__ FA_INLINE inline void dkdv8_body(const BwdParams& p, const int n_ktil
     // NBL bias loads issued after them are in flight (vector loads complete in
     // order; the dBias stores, issued before the copies, only add to the
     // count).  A partial wait may count only loads issued after the ones it
-    // guards: stores complete out of order with respect to loads (issued
-    // after the copies and counted in the wait, the dS stores let the barrier
-    // pass with copies in flight: NaN in dK and dBias at B=4, S=4096)
+    // guards: issued after the copies and counted in the wait, the dS stores
+    // gave NaN in dK and dBias at B=4, S=4096 (the barrier passed with copies
+    // in flight; stores evidently complete out of order with respect to loads)
     constexpr int NBL = BIAS ? 16 : 0;
     auto sync_copies = [&]() {
         wait_vmem_below<NBL>();
