@@ -342,6 +342,51 @@ def test_bias_long_causal():
     check(q, k, v, do, True, D ** -0.5, bias, [t.cpu() for t in outs], label="long causal")
 
 
+
+@pytest.mark.parametrize("kind", ["full", "heads"])
+def test_bias_dbias_full_size(kind):
+    # The benchmark's bias workloads, B=4, S=4096, H=32, D=128 bf16 causal with
+    # a (B, H, S, S) bias ("full") or a (1, H, S, S) one whose gradient sums
+    # the batch ("heads", through per-batch parts), and their gradients: a
+    # race between the tile copies and the waits that guard them shows at
+    # this size and not at the small ones.  No output may be non-finite; dK /
+    # dV equal those of the backward without a gradient bit for bit (the dS
+    # stores change no arithmetic) and dQ (from the stored dS) theirs within 2
+    # bf16 ulp; dBias of two heads against float32 torch math from the
+    # kernel's own O and LSE (within 1% of its largest magnitude; exactly 0
+    # above the diagonal).
+    B, S, H, D = 4, 4096, 32, 128
+    say(f"case: bias + dbias full size B=4 S=4096 H=32 D=128 bf16 causal, {kind}")
+    g = torch.Generator(DEV).manual_seed(31)
+    q, k, v, do = (torch.randn(B, S, H, D, generator=g, device=DEV).to(torch.bfloat16) for _ in range(4))
+    bias = (torch.randn(B if kind == "full" else 1, H, S, S, generator=g, device=DEV) * 2.0).to(torch.bfloat16)
+    scale = D ** -0.5
+    o, lse, _ = _lib.fwd(q, k, v, True, scale, bias=bias)
+    dq, dk, dv, db = _lib.bwd(q, k, v, o, do, lse, True, scale, bias=bias, want_dbias=True)
+    dq2, dk2, dv2 = _lib.bwd(q, k, v, o, do, lse, True, scale, bias=bias)
+    torch.cuda.synchronize()
+    assert db.shape == bias.shape
+    for n, t in (("O", o), ("LSE", lse), ("dQ", dq), ("dK", dk), ("dV", dv), ("dBias", db)):
+        assert torch.isfinite(t.float()).all(), n
+    assert torch.equal(dk, dk2) and torch.equal(dv, dv2)
+    ulp = 2.0 ** -7  # bfloat16
+    assert ((dq.float() - dq2.float()).abs() <= 2 * ulp * dq2.float().abs() + 1e-6).all()
+    mask = torch.ones(S, S, dtype=torch.bool, device=DEV).triu(1)
+    for b, h in ((0, 0), (3, 31)):
+        ref = torch.zeros(S, S, device=DEV)
+        for bb in ((b,) if kind == "full" else range(B)):
+            qs, ks, vs, dos, os_ = (t[bb, :, h].float() for t in (q, k, v, do, o))
+            st = qs @ ks.T * scale + bias[bb if kind == "full" else 0, h].float()
+            st.masked_fill_(mask, -float("inf"))
+            pm = torch.exp(st - lse[bb, h].float()[:, None])
+            ref += pm * (dos @ vs.T - (dos * os_).sum(1, keepdim=True))
+        bo = b if kind == "full" else 0
+        got = db[bo, h].float()
+        assert torch.equal(got[mask], torch.zeros_like(got[mask])), (bo, h)
+        err = (got - ref).abs().max().item()
+        say(f"  dBias[{bo},{h}] max err {err:.3g} of max {ref.abs().max().item():.3g}")
+        assert err <= 0.01 * ref.abs().max().item(), (bo, h, err)
+
 # Grids of at least 256 workgroups of 256 queries with a 16-bit bias and no
 # dropout take the forward whose waves stage their bias rows through LDS; the
 # small cases above do not.  O and LSE of a subset of heads against the
