@@ -306,7 +306,9 @@ def test_bwd_stages_on_two_streams(with_bias):
     for want_db in ((False, True) if with_bias else (False,)):
         ref = _lib.bwd(q, k, v, o, do, lse, True, D ** -0.5, bias=pb, want_dbias=want_db)
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-        db = torch.empty(1, H, S, 336, device=DEV)[..., :S] if want_db else None
+        # the gradient in the bias dtype, as _lib.bwd makes it (a float32 one
+        # sums float32 parts, a bf16 one bf16 parts: not the same bits)
+        db = torch.empty(1, H, S, 336, device=DEV, dtype=torch.bfloat16)[..., :S] if want_db else None
         a = _lib.bwd_args(q, k, v, o, do, lse, dq, dk, dv, True, D ** -0.5, 0.0, 0, 0, pb, db)
         ws = torch.empty(lib.fa_bwd_workspace_size(ctypes.byref(a)), device=DEV, dtype=torch.uint8)
         wsp = ctypes.c_void_p(ws.data_ptr())
@@ -323,4 +325,4 @@ def test_bwd_stages_on_two_streams(with_bias):
         torch.cuda.synchronize()
         assert torch.equal(dq, ref[0]) and torch.equal(dk, ref[1]) and torch.equal(dv, ref[2])
         if want_db:
-            assert torch.equal(db.to(torch.bfloat16), ref[3])
+            assert torch.equal(db, ref[3])
