@@ -164,9 +164,9 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
     const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
     // key block kt = 0 sees the most queries (causal): rank order is kt order
     const int2 tord = tile_order<32 * ((std::is_void<TB>::value || D <= 64) && !(Elem<T>::kF32 && D == 128) && D <= 128 ? 2 : 1)>(n_ktiles);
-    const int bhk = tord.x;
     const int kt = tord.y;
-    const int hk = bhk % p.Hkv, b = bhk / p.Hkv;
+    const int2 sbh = slice_bh(tord.x, p.Hkv, p.B, !std::is_void<TB>::value && p.bias_sb == 0);
+    const int hk = sbh.y, b = sbh.x;
     const int k0 = kt * C::BK;
     const int kw0 = k0 + 32 * w;
     const int kj = kw0 + l32;  // this lane's key
@@ -1041,9 +1041,9 @@ __device__ FA_INLINE inline void dkdv8_body(const BwdParams& p, const int n_ktil
     const int kb = w & 3;   // key block
     const int st = w >> 2;  // query sub-step of every tile
     const int2 tord = tile_order<32>(n_ktiles, bid, nblocks);  // kt = 0 sees the most queries
-    const int bhk = tord.x;
     const int kt = tord.y;
-    const int hk = bhk % p.Hkv, b = bhk / p.Hkv;
+    const int2 sbh = slice_bh(tord.x, p.Hkv, p.B, BIAS && p.bias_sb == 0);
+    const int hk = sbh.y, b = sbh.x;
     const int k0 = kt * C::BK;
     const int kw0 = k0 + 32 * kb;
     const int kj = kw0 + l32;  // this lane's key
@@ -1388,9 +1388,9 @@ __device__ FA_INLINE inline void dq_body(const BwdParams& p, const int n_qtiles,
     // w: the wave's 32-query block, sp: its key split (compile-time 0 without one)
     const int w = KS == 1 ? wg : wg & 3, sp = KS == 1 ? 0 : wg >> 2;
     const int2 tord = tile_order<32 * (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)>(n_qtiles, bid, nblocks);
-    const int bh = tord.x;
     const int qt = n_qtiles - 1 - tord.y;  // longest causal rows first
-    const int h = bh % p.H, b = bh / p.H;
+    const int2 sbh = slice_bh(tord.x, p.H, p.B, !std::is_void<TB>::value && p.bias_sb == 0);
+    const int h = sbh.y, b = sbh.x;
     const int hk = h / p.group;
     const int q0 = qt * C::BM;
     const int qw0 = q0 + 32 * w;

@@ -354,6 +354,14 @@ __device__ FA_INLINE inline int2 tile_order(int n_tiles) {
     return tile_order<SLOTS>(n_tiles, (int)blockIdx.x, (int)gridDim.x);
 }
 
+// (batch, head) of slice s of the B x NH slices: batch-major (s = b NH + h),
+// or head-major (s = h B + b) for a kernel that reads a bias shared by the
+// batches (batch stride 0): a group of slices (tile_order) then holds batches
+// of one head, which read the same bias rows through the XCD's L2
+__device__ FA_INLINE inline int2 slice_bh(int s, int NH, int B, bool head_major) {
+    return head_major ? make_int2(s % B, s / B) : make_int2(s / NH, s % NH);
+}
+
 // ---------------------------------------------------------------------------
 // Raw buffer view of the rows [0, min(nvalid, R)) of a tile of R rows in a
 // row-strided [rows][D] slice: loads at byte offsets past the last valid row

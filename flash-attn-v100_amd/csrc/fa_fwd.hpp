@@ -87,9 +87,9 @@ __global__ __launch_bounds__(256 * KS * QG, KS == 1 && QG == 1 && D <= 128 ? 2 :
     const int qg = QG == 1 ? 0 : wg >> 2;
 
     const int2 tord = tile_order<32 * (KS == 1 && QG == 1 && D <= 128 ? 2 : 1)>(p.n_qtiles);
-    const int bh = tord.x;
     const int qt = p.n_qtiles - 1 - tord.y;  // longest causal rows first
-    const int h = bh % p.H, b = bh / p.H;
+    const int2 sbh = slice_bh(tord.x, p.H, p.B, !std::is_void<TB>::value && p.bias_sb == 0);
+    const int h = sbh.y, b = sbh.x;
     const int hk = h / p.group;
     const int q0 = qt * C::BM * QG;  // the workgroup's first query
     const int qw0 = q0 + C::BM * qg + 32 * w;
