@@ -387,9 +387,10 @@ def bwd(q, k, v, o, do, lse, causal: bool, scale: float, dropout_p: float = 0.0,
         B, Sq, H, _ = q.shape
         Sk = k.shape[1]
         # batch / head dimensions the bias broadcasts are summed by the library;
-        # every element is written (zeros where causal masks).  Summed rows are
-        # 16-byte aligned (padded to 4 keys).  The library writes the caller's
-        # dtype directly unless a query-dimension sum is left to do here (in fp32).
+        # every element is written (zeros where causal masks).  A summed
+        # gradient's rows are padded to a multiple of 4 keys (the library's rule
+        # for its strides).  The library writes the caller's dtype directly unless
+        # a query-dimension sum is left to do here (in fp32).
         Bo = 1 if pb.shape[0] == 1 else B
         Ho = 1 if pb.shape[1] == 1 else H
         gdt = pb.dtype if (pb.dtype in DTYPE_CODES and (pb.shape[2] != 1 or Sq == 1)) else torch.float32
