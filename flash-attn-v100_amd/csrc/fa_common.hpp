@@ -363,6 +363,15 @@ __device__ FA_INLINE inline int2 tile_order(int n_tiles, int bid, int nblocks) {
     const int rank = r / gg;
     return make_int2(g * G + (r - rank * gg), rank);
 }
+// On the host: whether tile_order's plain group size leaves an XCD a last
+// group smaller than the others, i.e. whether FIT changes it
+inline bool host_group_uneven(int slots, int n_tiles, int nblocks) {
+    const int per_xcd = (nblocks >> 3) / n_tiles;
+    const int xcd_slices = per_xcd > 1 ? per_xcd : 1;
+    const int fill = (2 * slots + n_tiles - 1) / n_tiles;
+    const int target = fill < 1 ? 1 : (fill < xcd_slices ? fill : xcd_slices);
+    return xcd_slices % target != 0;
+}
 template <int SLOTS, bool FIT = true>
 __device__ FA_INLINE inline int2 tile_order(int n_tiles) {
     return tile_order<SLOTS, FIT>(n_tiles, (int)blockIdx.x, (int)gridDim.x);

@@ -38,6 +38,11 @@ CASES = [
     (torch.bfloat16, 2, 4500, 3000, 32, 8, True),     # causal with Sq > Sk (top-left)
     (torch.bfloat16, 1, 16461, 16461, 16, 2, True),   # causal, long rows, GQA 8:1
     (torch.float16, 1, 3100, 3100, 48, 48, True),     # causal, the smallest rows and grid routed here
+    # causal grids whose XCD share of slices (8 and 6) the plain slice-group
+    # size (6 and 4) does not divide: the launcher takes the instantiation
+    # that searches for a divisor (the case above, 6 and 5, is one too)
+    (torch.bfloat16, 2, 3072, 3072, 32, 32, True),
+    (torch.float16, 3, 4096, 4096, 16, 4, True),
 ]
 
 
