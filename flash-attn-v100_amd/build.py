@@ -23,7 +23,7 @@ OBJDIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "flash_attention_v100", "libfa_gfx950.so")
 ARCH = "gfx950"
 
-SOURCES = ["fa_abi.cpp", "fa_misc.hip"] + [
+SOURCES = ["fa_abi.cpp", "fa_misc.hip", "fa_fwd_fit.hip"] + [
     f"fa_{pas}_{mode}{dt}.hip"
     for pas in ("bwd", "fwd")  # the backward units take longest: start them first
     for mode, dts in (("d256_", ("bf16", "f16")), ("", ("bf16", "f16", "f32")), ("bias_", ("bf16", "f16", "f32")),

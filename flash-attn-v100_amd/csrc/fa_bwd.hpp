@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256, ((std::is_void<TB>::value || D <= 64) && !(Ele
     // wave index as a scalar: loop bounds derived from it stay wave-uniform
     const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
     // key block kt = 0 sees the most queries (causal): rank order is kt order
-    const int2 tord = tile_order<32 * ((std::is_void<TB>::value || D <= 64) && !(Elem<T>::kF32 && D == 128) && D <= 128 ? 2 : 1)>(n_ktiles);
+    const int2 tord = tile_order<32 * ((std::is_void<TB>::value || D <= 64) && !(Elem<T>::kF32 && D == 128) && D <= 128 ? 2 : 1), CAUSAL>(n_ktiles);
     const int kt = tord.y;
     const int2 sbh = slice_bh(tord.x, p.Hkv, p.B, !std::is_void<TB>::value && p.bias_sb == 0);
     const int hk = sbh.y, b = sbh.x;
@@ -594,7 +594,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_pp_kernel(const BwdParams p, cons
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
     const int grp = w >> 2, w4 = w & 3;
-    const int2 tord = tile_order<32>(n_ktiles);
+    const int2 tord = tile_order<32, CAUSAL>(n_ktiles);
     const int bhk = tord.x;
     const int kt = tord.y;
     const int hk = bhk % p.Hkv, b = bhk / p.Hkv;
@@ -1040,7 +1040,7 @@ __device__ FA_INLINE inline void dkdv8_body(const BwdParams& p, const int n_ktil
     const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
     const int kb = w & 3;   // key block
     const int st = w >> 2;  // query sub-step of every tile
-    const int2 tord = tile_order<32>(n_ktiles, bid, nblocks);  // kt = 0 sees the most queries
+    const int2 tord = tile_order<32, CAUSAL>(n_ktiles, bid, nblocks);  // kt = 0 sees the most queries
     const int kt = tord.y;
     const int2 sbh = slice_bh(tord.x, p.Hkv, p.B, BIAS && p.bias_sb == 0);
     const int hk = sbh.y, b = sbh.x;
@@ -1387,7 +1387,7 @@ __device__ FA_INLINE inline void dq_body(const BwdParams& p, const int n_qtiles,
     const int lane = tid & 63, wg = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
     // w: the wave's 32-query block, sp: its key split (compile-time 0 without one)
     const int w = KS == 1 ? wg : wg & 3, sp = KS == 1 ? 0 : wg >> 2;
-    const int2 tord = tile_order<32 * (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1)>(n_qtiles, bid, nblocks);
+    const int2 tord = tile_order<32 * (KS == 1 ? DqCfg<T, D>::MIN_BLOCKS : 1), CAUSAL>(n_qtiles, bid, nblocks);
     const int qt = n_qtiles - 1 - tord.y;  // longest causal rows first
     const int2 sbh = slice_bh(tord.x, p.H, p.B, !std::is_void<TB>::value && p.bias_sb == 0);
     const int h = sbh.y, b = sbh.x;
@@ -1856,7 +1856,7 @@ __global__ __launch_bounds__(512, 1) void dq_pp_kernel(const BwdParams p) {
     const int grp = w >> 2, w4 = w & 3;
     const int blk = 2 * w4 + grp;
     const int n_qtiles = (p.Sq + C::BM - 1) / C::BM;
-    const int2 tord = tile_order<32>(n_qtiles);
+    const int2 tord = tile_order<32, CAUSAL>(n_qtiles);
     const int bh = tord.x;
     const int qt = n_qtiles - 1 - tord.y;  // longest causal rows first
     const int h = bh % p.H, b = bh / p.H;
@@ -2256,7 +2256,7 @@ __global__ __launch_bounds__(256, 2) void dq_ds_kernel(const BwdParams p, const 
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31, hi = lane >> 5;
-    const int2 tord = tile_order<64>(n_qtiles);
+    const int2 tord = tile_order<64, CAUSAL>(n_qtiles);
     const int bh = tord.x;
     const int qt = n_qtiles - 1 - tord.y;  // longest causal rows first
     const int h = bh % p.H, b = bh / p.H;

@@ -332,30 +332,34 @@ __device__ FA_INLINE inline int xcd_remap(int L, int N) {
 // makes one group about fill the XCD's workgroup slots twice (SLOTS = 32 CUs
 // x resident workgroups per CU; measured against once and 4 times), so the
 // resident workgroups span few slices (K / V / Q tiles shared through the
-// XCD's L2), and a group never spans two XCDs.  With FIT, G is lowered (to at
-// most half) to a divisor of the XCD's slices: a small last group ran its long
-// tiles after the others had drained (measured, causal, outputs unchanged:
+// XCD's L2), and a group never spans two XCDs.  With FIT (the kernels pass it
+// for causal masking: tiles of one length balance in any order), G is lowered
+// (to at most half) to a divisor of the XCD's slices: a small last group ran
+// its long tiles after the others had drained (measured, causal, outputs unchanged:
 // 2 x 3072 x 32 heads and 3 x 4096 x 16 heads at D = 128, 7-11% per step;
 // 2 x 4096 x 24 heads at D = 64, 6%).
 // (bid, nblocks: the workgroup's index among the nblocks of its kind, for a
 // launch that runs two kinds of workgroups)
-template <int SLOTS, bool FIT = true>
+template <int SLOTS, bool FIT>
 __device__ FA_INLINE inline int2 tile_order(int n_tiles, int bid, int nblocks) {
     const int L = xcd_remap(bid, nblocks);
     const int n_slices = nblocks / n_tiles;
     // groups stay inside one XCD's share of the slices
     const int xcd_slices = max(1, (nblocks >> 3) / n_tiles);
-    const int target = max(1, min(xcd_slices, (2 * SLOTS + n_tiles - 1) / n_tiles));
-    // FIT: the largest group size down to half the target (at most 63 below
-    // it) that divides the XCD's slices, so that its last group is as large as
-    // the others: lane i tests target - i.  (A scalar search loop here raised
-    // the kernels' scalar-register pressure into lane spills inside their tile
-    // loops.)
-    const int lane = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
-    const int c = target - lane;
-    const bool divides = 2 * c >= target && (int)((unsigned)xcd_slices % (unsigned)max(c, 1)) == 0;
-    const unsigned long long hits = __builtin_amdgcn_ballot_w64(divides);
-    const int G = FIT && hits ? target - (int)__builtin_ctzll(hits) : target;
+    int G = max(1, min(xcd_slices, (2 * SLOTS + n_tiles - 1) / n_tiles));
+    if constexpr (FIT) {
+        // the largest group size down to half this target (at most 63 below
+        // it) that divides the XCD's slices, so that its last group is as large
+        // as the others: lane i tests G - i.  (A scalar search loop here raised
+        // the kernels' scalar-register pressure into lane spills inside their
+        // tile loops; without FIT no trace of the search is compiled, as even
+        // its unused form moved the copy-wave forward's prologue, 1-2% slower.)
+        const int lane = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+        const int c = G - lane;
+        const bool divides = 2 * c >= G && (int)((unsigned)xcd_slices % (unsigned)max(c, 1)) == 0;
+        const unsigned long long hits = __builtin_amdgcn_ballot_w64(divides);
+        if (hits) G -= (int)__builtin_ctzll(hits);
+    }
     const int per_group = G * n_tiles;
     const int g = L / per_group;
     const int r = L - g * per_group;
@@ -372,7 +376,7 @@ inline bool host_group_uneven(int slots, int n_tiles, int nblocks) {
     const int target = fill < 1 ? 1 : (fill < xcd_slices ? fill : xcd_slices);
     return xcd_slices % target != 0;
 }
-template <int SLOTS, bool FIT = true>
+template <int SLOTS, bool FIT>
 __device__ FA_INLINE inline int2 tile_order(int n_tiles) {
     return tile_order<SLOTS, FIT>(n_tiles, (int)blockIdx.x, (int)gridDim.x);
 }

@@ -86,7 +86,10 @@ __global__ __launch_bounds__(256 * KS * QG, KS == 1 && QG == 1 && D <= 128 ? 2 :
     const int w = KS == 1 && QG == 1 ? wg : wg & 3, sp = KS == 1 ? 0 : wg >> 2;
     const int qg = QG == 1 ? 0 : wg >> 2;
 
-    const int2 tord = tile_order<32 * (KS == 1 && QG == 1 && D <= 128 ? 2 : 1)>(p.n_qtiles);
+    // without the divisor search for a bias: at 4 x 4096 x 32 heads with a
+    // full bias, where it keeps the group size, this kernel's code moved with
+    // it and ran 1.7% slower
+    const int2 tord = tile_order<32 * (KS == 1 && QG == 1 && D <= 128 ? 2 : 1), CAUSAL && std::is_void<TB>::value>(p.n_qtiles);
     const int qt = p.n_qtiles - 1 - tord.y;  // longest causal rows first
     const int2 sbh = slice_bh(tord.x, p.H, p.B, !std::is_void<TB>::value && p.bias_sb == 0);
     const int h = sbh.y, b = sbh.x;
@@ -886,6 +889,12 @@ __global__ __launch_bounds__(576, 1) void fwd_pp_kernel(const FwdParams p) {
 // -12%, (1, 8192, 16) -14%, (2, 3072, 32) -6%; (1, 4096, 16) and (1, 8192, 8)
 // (256 workgroups) +3%, (4, 2048, 32) and (2, 2048, 64) equal, (8, 1024, 32)
 // +3%.
+// The causal fwd_pp_kernel with FIT (D = 128), instantiated in a translation
+// unit of its own (fa_fwd_fit.hip): compiled beside the plain one, it moved
+// the plain one's prologue and that ran 1% slower at 4 x 4096 x 32 heads
+template <typename T>
+hipError_t launch_fwd_pp_fit(const FwdParams& q, int64_t nblocks, hipStream_t s);
+
 inline bool fwd_pp_wanted(const FwdParams& p, bool causal) {
     const int64_t n = (int64_t)((p.Sq + 255) / 256) * p.H * p.B;
     return n >= 256 && (!causal || (p.Sq >= 3072 && n >= 512));
@@ -902,10 +911,7 @@ hipError_t launch_fwd_t(const FwdParams& p, hipStream_t s) {
             // causal rows differ in length, so a small last slice group runs
             // its long rows alone: (2, 3072, 32) 173.0 -> 155.7 us with FIT
             if constexpr (CAUSAL) {
-                if (host_group_uneven(32, q.n_qtiles, (int)nblocks)) {
-                    hipLaunchKernelGGL((fwd_pp_kernel<T, D, true, true>), dim3((unsigned)nblocks), dim3(CP::NT), 0, s, q);
-                    return hipGetLastError();
-                }
+                if (host_group_uneven(32, q.n_qtiles, (int)nblocks)) return launch_fwd_pp_fit<T>(q, nblocks, s);
             }
             hipLaunchKernelGGL((fwd_pp_kernel<T, D, CAUSAL, false>), dim3((unsigned)nblocks), dim3(CP::NT), 0, s, q);
             return hipGetLastError();
