@@ -86,9 +86,9 @@ __global__ __launch_bounds__(256 * KS * QG, KS == 1 && QG == 1 && D <= 128 ? 2 :
     const int w = KS == 1 && QG == 1 ? wg : wg & 3, sp = KS == 1 ? 0 : wg >> 2;
     const int qg = QG == 1 ? 0 : wg >> 2;
 
-    // without the divisor search for a bias: at 4 x 4096 x 32 heads with a
-    // full bias, where it keeps the group size, this kernel's code moved with
-    // it and ran 1.7% slower
+    // the divisor search for causal masking without a bias: the biased forward
+    // keeps its code (measured 4 x 4096 x 32 heads with a full bias, where the
+    // search keeps the group size, it was no faster)
     const int2 tord = tile_order<32 * (KS == 1 && QG == 1 && D <= 128 ? 2 : 1), CAUSAL && std::is_void<TB>::value>(p.n_qtiles);
     const int qt = p.n_qtiles - 1 - tord.y;  // longest causal rows first
     const int2 sbh = slice_bh(tord.x, p.H, p.B, !std::is_void<TB>::value && p.bias_sb == 0);
