@@ -890,8 +890,9 @@ __global__ __launch_bounds__(576, 1) void fwd_pp_kernel(const FwdParams p) {
 // (256 workgroups) +3%, (4, 2048, 32) and (2, 2048, 64) equal, (8, 1024, 32)
 // +3%.
 // The causal fwd_pp_kernel with FIT (D = 128), instantiated in a translation
-// unit of its own (fa_fwd_fit.hip): compiled beside the plain one, it moved
-// the plain one's prologue and that ran 1% slower at 4 x 4096 x 32 heads
+// unit of its own (fa_fwd_fit.hip), so that the units of the plain kernels
+// compile the same code as without it (their prologues' instruction order
+// has moved with unrelated changes, and the forward's speed with it)
 template <typename T>
 hipError_t launch_fwd_pp_fit(const FwdParams& q, int64_t nblocks, hipStream_t s);
 
